@@ -1,0 +1,83 @@
+"""ctypes binding of libfsamp.so (the C ABI in include/fsamp.h).
+
+The library is loaded from this package directory; there is no fallback: a missing or
+unloadable library raises, so nothing can silently run another implementation.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG, "libfsamp.so")
+
+DTYPE_F16 = 0
+DTYPE_BF16 = 1
+K_MAX = 1024
+
+# every function the header declares, with (restype, argtypes)
+_vp, _i32, _i64, _u64, _dbl, _sz = (ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64,
+                                    ctypes.c_uint64, ctypes.c_double, ctypes.c_size_t)
+
+
+class Plan(ctypes.Structure):
+    _fields_ = [("batch", _i64), ("vocab", _i64), ("k", _i64), ("splits", _i32),
+                ("slice", _i32), ("threads", _i32), ("chunks", _i32), ("vec", _i32),
+                ("reserved", _i32), ("workspace_bytes", _sz)]
+
+
+class AttrRow(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char * 64), ("threads", _i32), ("chunks", _i32),
+                ("vgprs", _i32), ("scratch_bytes", _i32), ("lds_bytes", _i32),
+                ("blocks_per_cu", _i32)]
+
+
+SIGNATURES = {
+    "fsamp_error_string": (ctypes.c_char_p, [_i32]),
+    "fsamp_make_plan": (_i32, [_vp, _i64, _i64, _i64, _i64, ctypes.POINTER(Plan)]),
+    "fsamp_workspace_bytes": (_sz, [_vp, _i64, _i64, _i64, _i64]),
+    "fsamp_workspace_init": (_i32, [_vp, _sz, _vp]),
+    "fsamp_sample": (_i32, [_vp, _i32, _i64, _i64, _i64, _dbl, _vp, _u64, _u64, _vp, _vp, _sz,
+                            _i64, _vp]),
+    "fsamp_stages": (_i32, [_vp, _i32, _i64, _i64, _i64, _dbl, _vp, _u64, _u64, _vp, _vp, _vp,
+                            _vp, _sz, _i64, _vp]),
+    "fsamp_topk": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _sz, _i64, _vp]),
+    "fsamp_probe_phase": (_i32, [_vp, _i32, _i64, _i64, _i64, _dbl, _i64, _vp, _vp, _sz, _i64,
+                                 _vp]),
+    "fsamp_probe_noop": (_i32, [_i64, _vp, _vp]),
+    "fsamp_probe_scan_rowblock": (_i32, [_vp, _i32, _i64, _i64, _vp, _vp]),
+    "fsamp_probe_scan_split": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _sz, _vp]),
+    "fsamp_kernel_attrs": (_i32, [ctypes.POINTER(AttrRow), _i32, ctypes.POINTER(_i32)]),
+    "fsamp_debug_force_threads": (_i32, [_i32]),
+}
+
+_lib = None
+
+
+def load():
+    """Load libfsamp.so and declare every entry point; raises if it is missing."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is not built: run `python -m llm_sampling_kernel_amd.build` "
+                "(the sampler has no non-HIP fallback)")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+class FsampError(RuntimeError):
+    def __init__(self, status: int):
+        self.status = status
+        super().__init__(load().fsamp_error_string(status).decode())
+
+
+def check(status: int) -> None:
+    if status != 0:
+        raise FsampError(status)

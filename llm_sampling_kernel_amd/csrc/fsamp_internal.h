@@ -1,0 +1,56 @@
+// fsamp_internal.h -- definitions shared by the sampler kernel and its host launcher.
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+
+namespace fsamp {
+
+constexpr int CAND_CAP = 4096;   // LDS candidate words per workgroup (32 KiB)
+constexpr int NSUB = 8;          // LDS sub-histograms in the radix fallback
+constexpr int RMAX = (FSAMP_K_MAX + 63) / 64;  // ranks per lane in the tail
+
+// Kernel arguments (passed by value as kernarg).
+struct Params {
+  const uint16_t* logits;  // [B, V] fp16/bf16 bit patterns
+  int64_t* out;            // [B] token ids (sample mode / ablation)
+  int64_t* ids;            // [B, K] candidate ids (topk mode) or nullptr
+  uint8_t* keep;           // [B, K] or nullptr
+  float* renormed;         // [B, K] or nullptr
+  const float* u;          // [B] uniforms or nullptr (splitmix64 of seed/offset/row)
+  uint64_t seed, offset;
+  uint64_t* partials;      // workspace: [B, S, K] per-split candidates
+  uint32_t* tickets;       // workspace: [B] arrival counters, zero between calls
+  int B, V, K, S;
+  int slice;               // elements per split, a multiple of 8
+  float top_p_f;           // (float)top_p
+  int keep_all;            // top_p >= 1: keep every rank
+  int is_bf16;
+  int vec;                 // rows are 16-byte aligned: dwordx4 loads
+  int stop;                // ablation phase (7 = the whole pipeline)
+};
+
+struct KernelEntry {
+  int threads;
+  int chunks;
+  int vec;
+  const void* fn;
+  const char* name;
+};
+
+// (threads, chunks) register tilings that are compiled; chunks*8 elements per thread.
+// Vector-load (16-byte aligned rows) tilings:
+#define FSAMP_KERNEL_LIST_VEC(X) \
+  X(256, 1) X(256, 2) X(256, 3) X(256, 4) X(256, 5) X(256, 6) X(256, 8) X(256, 12) X(256, 16) \
+  X(512, 20) X(512, 24) X(512, 32) X(512, 38) \
+  X(1024, 4) X(1024, 5) X(1024, 6) X(1024, 8) X(1024, 10) X(1024, 12) X(1024, 16) X(1024, 19)
+// Element-load tilings (rows not 16-byte aligned, V % 8 != 0): small slices only; the planner
+// adds splits until a slice fits.
+#define FSAMP_KERNEL_LIST_SCALAR(X) \
+  X(256, 1) X(256, 2) X(256, 3) X(256, 4) X(256, 6) X(256, 8) X(1024, 4) X(1024, 5) \
+  X(1024, 6) X(1024, 8)
+
+extern const KernelEntry kKernels[];
+extern const int kNumKernels;
+
+}  // namespace fsamp

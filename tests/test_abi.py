@@ -1,0 +1,92 @@
+"""CPU checks of the C ABI: the library loads, exports every entry point include/fsamp.h
+declares, and its host-side planning and argument checks behave (no kernel is launched)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from llm_sampling_kernel_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "fsamp.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fsamp_[a-z_]+)\s*\(", text)))
+
+
+def test_header_declares_the_reference_surface():
+    names = declared_functions()
+    for want in ("fsamp_sample", "fsamp_topk", "fsamp_stages", "fsamp_probe_phase",
+                 "fsamp_probe_noop", "fsamp_probe_scan_rowblock", "fsamp_probe_scan_split",
+                 "fsamp_kernel_attrs"):
+        assert want in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+
+
+def plan(B, V, k, splits=0, ptr=4096):
+    p = _lib.Plan()
+    rc = _lib.load().fsamp_make_plan(ctypes.c_void_p(ptr), B, V, k, splits, ctypes.byref(p))
+    return rc, p
+
+
+@pytest.mark.parametrize("B,V,k,S,threads", [
+    (1, 151936, 50, 32, 256),     # C1: 32 splits of 4752 elements
+    (64, 128256, 50, 4, 256),     # C2, B=64
+    (16, 151936, 1024, 4, 1024),  # C4 k=1024: 4 splits, 4096 merged words
+    (256, 151936, 50, 1, 1024),   # C5: one workgroup per row, slice in VGPRs
+])
+def test_plans_for_the_benchmark_shapes(B, V, k, S, threads):
+    rc, p = plan(B, V, k)
+    assert rc == 0 and p.splits == S and p.threads == threads
+    assert p.threads * p.chunks * 8 >= p.slice and p.slice * p.splits >= V
+    assert p.slice % 8 == 0 and p.vec == 1
+    assert p.workspace_bytes == (0 if S == 1 else ((4 * B + 255) // 256) * 256 + B * S * k * 8)
+
+
+def test_every_plan_tiles_its_slice_and_fits_the_merge_buffer():
+    for B in (1, 2, 7, 16, 64, 127, 128, 300):
+        for V in (1, 7, 8, 30, 1000, 4001, 32000, 128256, 151936, 262143, 262144):
+            for k in (1, 20, 50, 256, 1024):
+                for splits in (0, 1, 3, 64):
+                    for ptr in (4096, 4098):
+                        rc, p = plan(B, V, k, splits, ptr)
+                        if min(k, V) > 1024:
+                            continue
+                        assert rc == 0, (B, V, k, splits, rc)
+                        assert p.threads * p.chunks * 8 >= p.slice
+                        assert p.splits * p.k <= 4096
+                        assert (p.splits - 1) * p.slice < V <= p.splits * p.slice
+                        assert p.vec == int(ptr % 16 == 0 and V % 8 == 0)
+
+
+def test_argument_checks_return_the_reference_messages():
+    lib = _lib.load()
+    assert plan(1, 100, 0)[0] == 3 and b"top_k must be >= 1" == lib.fsamp_error_string(3)
+    assert plan(1, 5000, 2000)[0] == 4 and b"top_k must be <= 1024" == lib.fsamp_error_string(4)
+    assert plan(0, 100, 5)[0] == 2
+    assert lib.fsamp_error_string(1) == b"logits must be float16 or bfloat16"
+    assert lib.fsamp_error_string(5) == b"top_p must be in (0, 1]"
+    assert lib.fsamp_error_string(2) == b"logits must be a contiguous cuda [B, V] tensor"
+    # the launch entry points check arguments before touching the device
+    null = ctypes.c_void_p(0)
+    assert lib.fsamp_sample(ctypes.c_void_p(4096), 2, 1, 100, 5, 0.9, None, 0, 0,
+                            ctypes.c_void_p(4096), None, 0, 0, null) == 1
+    assert lib.fsamp_sample(ctypes.c_void_p(4096), 1, 1, 100, 5, 1.5, None, 0, 0,
+                            ctypes.c_void_p(4096), None, 0, 0, null) == 5
+    assert lib.fsamp_sample(ctypes.c_void_p(4096), 1, 1, 151936, 50, 0.9, None, 0, 0,
+                            ctypes.c_void_p(4096), None, 0, 0, null) == 6  # workspace needed
+    assert lib.fsamp_probe_phase(ctypes.c_void_p(4096), 1, 1, 100, 5, 0.9, 8,
+                                 ctypes.c_void_p(4096), None, 0, 0, null) == 8
+    assert lib.fsamp_probe_scan_split(ctypes.c_void_p(4096), 1, 1, 100, 0,
+                                      ctypes.c_void_p(4096), None, 0, null) == 9

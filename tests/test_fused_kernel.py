@@ -1,0 +1,442 @@
+"""GPU parity and behaviour tests of the HIP sampler (libfsamp.so through fused_sampling).
+
+Mirrors the reference's tests/test_fused_kernel.py (cited per test) with the CPU oracle
+(oracle/fsamp_oracle.c) in place of benchmarks/reference.py.  The oracle's fp32 tail fixes
+the same evaluation order as the kernel's, so candidate ids, keep masks, renormed
+probabilities and token ids are compared bit for bit, not within a tolerance.
+"""
+
+import math
+import os
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from llm_sampling_kernel_amd import _lib, fused, fused_sampling  # noqa: E402
+from llm_sampling_kernel_amd import workloads as W  # noqa: E402
+from oracle import oracle as O  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+DTYPES = ["float16", "bfloat16"]
+TORCH_DTYPE = {"float16": torch.float16, "bfloat16": torch.bfloat16}
+
+
+def dev(bits: np.ndarray, dtype: str) -> torch.Tensor:
+    t = torch.from_numpy(np.ascontiguousarray(bits).view(np.int16))
+    return t.view(TORCH_DTYPE[dtype]).cuda()
+
+
+def bits_of(x: torch.Tensor) -> np.ndarray:
+    return x.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def randn_bits(shape, seed, scale, dtype):
+    x = np.random.Generator(np.random.PCG64(seed)).standard_normal(shape).astype(np.float32)
+    return W.to_bits(x * scale, dtype)
+
+
+def ustream(B, seed):
+    return np.random.Generator(np.random.PCG64(seed)).random(B, dtype=np.float32)
+
+
+def oracle(bits, dtype, k, p, u):
+    return O.sample(bits, dtype, k, p, u, return_stages=True, nthreads=8)
+
+
+def run_u(x, k, p, u_np, splits=0):
+    u = torch.from_numpy(u_np).cuda()
+    tok = fused.sample_fused_u(x, k, p, u, splits)
+    ids, keep, ren = fused_sampling.stages_fused_u(x, k, p, u, splits)
+    torch.cuda.synchronize()
+    return tok.cpu().numpy(), ids.cpu().numpy(), keep.cpu().numpy(), ren.cpu().numpy()
+
+
+def rank_of(topk_ids, tok):
+    return (topk_ids == tok[:, None]).argmax(-1)
+
+
+def test_the_sampler_runs_from_the_in_tree_hip_library():
+    lib = _lib.load()
+    assert os.path.dirname(os.path.abspath(lib._name)) == os.path.dirname(_lib.__file__)
+    x = torch.zeros(2, 64, device="cuda", dtype=torch.bfloat16)
+    assert fused.topk_fused(x, 3).tolist() == [[0, 1, 2]] * 2
+
+
+# --- the five benchmark configurations, full size ---------------------------------------------
+
+FIX = np.load(os.path.join(HERE, "golden", "workloads.npz"))
+
+
+@pytest.mark.parametrize("name", W.CASE_NAMES)
+def test_workload_parity_with_the_golden_fixture_and_the_oracle(name):
+    c = W.case(name)
+    assert c.digest() == bytes(FIX[f"{name}/digest"]).decode(), "seeded inputs differ"
+    x = dev(c.logits, c.dtype)
+    ids = fused.topk_fused(x, c.top_k).cpu().numpy()
+    assert np.array_equal(ids, FIX[f"{name}/topk_ids"]), "candidate set or order differs"
+    tok, _, keep, ren = run_u(x, c.top_k, c.top_p, c.u)
+    assert np.array_equal(tok, FIX[f"{name}/token_ids"]), "token ids differ"
+    assert np.array_equal(keep.sum(-1), FIX[f"{name}/cutoff"]), "nucleus size differs"
+    s = oracle(c.logits, c.dtype, c.top_k, c.top_p, c.u)
+    assert np.array_equal(ren.view(np.uint32), s.renormed.view(np.uint32)), "renormed bits differ"
+    # retained mass against fp64: within 1e-5 relative
+    p64, c64, _, cut64 = O.stages_f64(c.logits, c.dtype, c.top_k, c.top_p)
+    zp = s.cumsum[np.arange(c.batch), s.cutoff - 1].astype(np.float64)
+    z64 = c64[np.arange(c.batch), cut64 - 1]
+    same = s.cutoff == cut64
+    assert same.mean() >= 0.95
+    assert (np.abs(zp - z64)[same] / z64[same]).max() < 1e-5
+
+
+def test_c5_properties_at_full_batch():
+    c = W.c5()
+    x = dev(c.logits, c.dtype)
+    ids = fused.topk_fused(x, 50)
+    # sortedness (non-increasing value along the row) and ids address their own values
+    vals = torch.gather(x.float(), 1, ids)
+    assert (vals[:, :-1] >= vals[:, 1:]).all()
+    assert (vals[:, -1:] >= x.float()).sum(-1).ge(50).all()
+    # idempotence: sampling twice with the same u gives the same tokens
+    u = torch.from_numpy(c.u).cuda()
+    assert torch.equal(fused.sample_fused_u(x, 50, 0.9, u), fused.sample_fused_u(x, 50, 0.9, u))
+
+
+# --- candidate set (reference tests/test_fused_kernel.py:29-45) --------------------------------
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("top_k", [1, 20, 50, 100, 1024])
+@pytest.mark.parametrize("vocab", [2000, 4001, 128256, 151936])
+def test_candidate_set_matches_the_oracle_exactly(vocab, top_k, dtype):
+    bits = randn_bits((16, vocab), vocab + top_k, 4.0, dtype)
+    got = fused.topk_fused(dev(bits, dtype), top_k).cpu().numpy()
+    want = oracle(bits, dtype, top_k, 0.9, np.zeros(16, np.float32)).topk_ids
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_all_equal_logits_resolve_to_the_lowest_token_ids(dtype):
+    x = torch.zeros(4, 4000, device="cuda", dtype=TORCH_DTYPE[dtype])
+    assert fused.topk_fused(x, 50).tolist() == [list(range(50))] * 4
+
+
+def test_plus_and_minus_zero_tie():
+    bits = np.array([[0x8000, 0x0000, 0x8000, 0x3F80, 0x0000, 0xBF80, 0x8000, 0x0000]], np.uint16)
+    x = dev(bits, "bfloat16")
+    assert fused.topk_fused(x, 8).tolist() == [[3, 0, 1, 2, 4, 6, 7, 5]]
+
+
+@pytest.mark.parametrize("vocab,splits", [(151936, 1), (151936, 8), (20000, 4), (5000, 1)])
+def test_ties_past_the_candidate_buffer_are_still_exact(vocab, splits):
+    # reference :132-141 -- every element ties, far more than the LDS candidate buffer holds
+    x = torch.zeros(2, vocab, device="cuda", dtype=torch.bfloat16)
+    for top_k in (1, 50, 100, 1024):
+        assert fused.topk_fused(x, top_k, splits=splits).tolist() == [list(range(top_k))] * 2
+
+
+@pytest.mark.parametrize("vocab", [20000, 151936])
+def test_dense_tie_rows_match_the_oracle_with_one_split(vocab):
+    # reference :144-151
+    bits = randn_bits((8, vocab), 44, 0.05, "bfloat16")
+    x = dev(bits, "bfloat16")
+    for top_k in (20, 50, 100, 1024):
+        want = oracle(bits, "bfloat16", top_k, 0.9, np.zeros(8, np.float32)).topk_ids
+        assert np.array_equal(fused.topk_fused(x, top_k, splits=1).cpu().numpy(), want)
+
+
+def test_tie_grid_rows_through_every_path():
+    # 64-value grid (C3-like) at every split count: filter path and radix fallback agree
+    c = W.c3()
+    x = dev(c.logits, c.dtype)
+    want = FIX["C3/topk_ids"]
+    for s in (1, 2, 3, 4, 8, 16, 32, 64):
+        assert np.array_equal(fused.topk_fused(x, 50, splits=s).cpu().numpy(), want), s
+
+
+def test_every_split_count_and_workgroup_size_gives_the_same_answer():
+    bits = randn_bits((4, 151936), 45, 3.0, "bfloat16")
+    x = dev(bits, "bfloat16")
+    u = ustream(4, 46)
+    want = oracle(bits, "bfloat16", 50, 0.9, u)
+    lib = _lib.load()
+    try:
+        for threads in (0, 256, 512, 1024):
+            _lib.check(lib.fsamp_debug_force_threads(threads))
+            for s in (1, 2, 5, 8, 19, 32, 81):
+                try:
+                    tok, ids, keep, ren = run_u(x, 50, 0.9, u, s)
+                except _lib.FsampError as e:
+                    assert e.status == 10  # this size cannot tile the slice: a clean refusal
+                    continue
+                assert np.array_equal(tok, want.token_ids), (threads, s)
+                assert np.array_equal(ren.view(np.uint32), want.renormed.view(np.uint32))
+    finally:
+        lib.fsamp_debug_force_threads(0)
+
+
+# --- sampling (reference :48-108) ---------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("top_p", [0.5, 0.90, 0.95, 1.0])
+def test_sampled_token_is_inside_the_oracle_nucleus(top_p, dtype):
+    bits = randn_bits((8, 151936), 50, 4.0, dtype)
+    x = dev(bits, dtype)
+    s = oracle(bits, dtype, 50, top_p, np.zeros(8, np.float32))
+    for off in range(32):
+        tok = fused.sample_fused(x, 50, top_p, offset=off).cpu().numpy()
+        hit = s.topk_ids == tok[:, None]
+        assert hit.any(-1).all()
+        assert (rank_of(s.topk_ids, tok) < s.cutoff).all()
+        # and exactly the oracle's draw for the same splitmix64 uniforms
+        u = O.rng_uniform(fused.DEFAULT_SEED, off, 8)
+        assert np.array_equal(tok, oracle(bits, dtype, 50, top_p, u).token_ids)
+
+
+def test_top_k_one_is_the_argmax_and_ignores_the_rng():
+    bits = randn_bits((8, 4000), 51, 4.0, "bfloat16")
+    x = dev(bits, "bfloat16")
+    expected = x.float().argmax(dim=-1)
+    for off in range(8):
+        assert torch.equal(fused.sample_fused(x, 1, 0.9, offset=off), expected)
+
+
+def test_one_hot_logits_always_sample_the_spike():
+    x = torch.full((8, 4000), -30.0, device="cuda", dtype=torch.bfloat16)
+    x[:, 1234] = 30.0
+    for off in range(8):
+        assert (fused.sample_fused(x, 50, 0.9, offset=off) == 1234).all()
+
+
+def test_sampling_frequencies_match_the_renormalized_distribution():
+    probs = [0.40, 0.30, 0.15, 0.10, 0.05]
+    n = 20000
+    row = torch.log(torch.tensor(probs, device="cuda"))
+    x = row.expand(n, 5).contiguous().to(torch.bfloat16)
+    tok = fused.sample_fused(x, 5, 1.0, offset=0).cpu().numpy()
+    s = oracle(bits_of(x), "bfloat16", 5, 1.0, np.zeros(n, np.float32))
+    freq = np.bincount(rank_of(s.topk_ids, tok), minlength=5) / n
+    assert np.abs(freq - s.renormed[0]).max() < 4 * math.sqrt(0.4 * 0.6 / n)
+
+
+def test_equal_logits_sample_close_to_uniform():
+    k, n = 8, 4096
+    x = torch.zeros(n, k, device="cuda", dtype=torch.bfloat16)
+    counts = torch.bincount(fused.sample_fused(x, k, 1.0, offset=0), minlength=k).float()
+    assert (counts > 0).all()
+    sigma = math.sqrt(n * (1 / k) * (1 - 1 / k))
+    assert (counts - n / k).abs().max().item() < 4 * sigma
+
+
+def test_the_top_p_cutoff_matches_the_oracle_cutoff():
+    bits = randn_bits((4, 4000), 52, 2.0, "bfloat16")
+    x = dev(bits, "bfloat16")
+    s = oracle(bits, "bfloat16", 50, 0.9, np.zeros(4, np.float32))
+    seen = np.zeros((4, 50), bool)
+    for off in range(4000):
+        tok = fused.sample_fused(x, 50, 0.90, offset=off).cpu().numpy()
+        seen[np.arange(4), rank_of(s.topk_ids, tok)] = True
+    assert np.array_equal(seen.sum(-1), s.cutoff)
+
+
+def test_same_seed_and_offset_reproduce_and_different_offsets_advance():
+    x = dev(randn_bits((64, 4000), 53, 4.0, "bfloat16"), "bfloat16")
+    a = fused.sample_fused(x, 50, 0.9, seed=7, offset=3)
+    assert torch.equal(a, fused.sample_fused(x, 50, 0.9, seed=7, offset=3))
+    assert not torch.equal(a, fused.sample_fused(x, 50, 0.9, seed=7, offset=4))
+    assert not torch.equal(a, fused.sample_fused(x, 50, 0.9, seed=8, offset=3))
+
+
+def test_generator_path_advances_and_reseeding_reproduces():
+    x = dev(randn_bits((64, 4000), 54, 4.0, "bfloat16"), "bfloat16")
+    torch.manual_seed(123)
+    a = fused.sample_fused(x, 50, 0.9)
+    b = fused.sample_fused(x, 50, 0.9)
+    assert not torch.equal(a, b)
+    torch.manual_seed(123)
+    assert torch.equal(a, fused.sample_fused(x, 50, 0.9))
+
+
+def test_rejects_shapes_and_dtypes_outside_the_regime():
+    x = torch.randn(2, 4000, device="cuda", dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="float16 or bfloat16"):
+        fused.sample_fused(x.float(), 50, 0.9)
+    with pytest.raises(RuntimeError, match=r"top_k must be <= 1024"):
+        fused.sample_fused(x, 2000, 0.9)
+    with pytest.raises(RuntimeError, match=r"top_k must be >= 1"):
+        fused.sample_fused(x, 0, 0.9)
+    with pytest.raises(RuntimeError, match=r"top_p must be in \(0, 1\]"):
+        fused.sample_fused(x, 50, 1.5)
+    with pytest.raises(RuntimeError, match="contiguous cuda"):
+        fused.sample_fused(x.t().contiguous().t(), 50, 0.9)
+    with pytest.raises(RuntimeError, match="contiguous cuda"):
+        fused.sample_fused(x.cpu(), 50, 0.9)
+
+
+# --- edge shapes ---------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("B,V,k", [(1, 1, 1), (3, 7, 50), (2, 30, 500), (5, 1024, 1024),
+                                   (1, 9, 8), (300, 4000, 50), (7, 4001, 100), (2, 100000, 1000)])
+def test_edge_shapes_match_the_oracle(B, V, k):
+    for dtype in DTYPES:
+        bits = randn_bits((B, V), B * 1000 + V, 3.0, dtype)
+        x = dev(bits, dtype)
+        u = ustream(B, V)
+        s = oracle(bits, dtype, k, 0.9, u)
+        tok, ids, keep, ren = run_u(x, k, 0.9, u)
+        assert np.array_equal(fused.topk_fused(x, k).cpu().numpy(), s.topk_ids)
+        assert np.array_equal(tok, s.token_ids)
+        assert np.array_equal(keep, s.keep)
+        assert np.array_equal(ren.view(np.uint32), s.renormed.view(np.uint32))
+
+
+def test_unaligned_rows_take_the_element_path():
+    bits = randn_bits((4, 20001), 55, 3.0, "bfloat16")
+    full = dev(bits.reshape(-1), "bfloat16")
+    x = full[1:20001].view(4, 5000)  # starts 2 bytes into an allocation
+    assert x.data_ptr() % 16 != 0
+    want = oracle(bits_of(x), "bfloat16", 50, 0.9, np.zeros(4, np.float32)).topk_ids
+    assert np.array_equal(fused.topk_fused(x, 50).cpu().numpy(), want)
+
+
+def test_masked_and_extreme_rows():
+    x = torch.randn(6, 5000, device="cuda") * 3
+    x[0, 100:] = float("-inf")
+    x[1, :] = -3e38
+    x[1, 7] = -1e38
+    x[2, :] = 3e38
+    x[3, ::3] = 0.0
+    x[4, :] = -0.0
+    x[5, 10:] = float("-inf")
+    for td in (torch.bfloat16,):
+        xx = x.to(td)
+        bits = bits_of(xx)
+        u = ustream(6, 56)
+        s = oracle(bits, "bfloat16", 100, 0.95, u)
+        tok, _, keep, ren = run_u(xx, 100, 0.95, u)
+        assert np.array_equal(tok, s.token_ids)
+        assert np.array_equal(keep, s.keep)
+        assert np.array_equal(ren.view(np.uint32), s.renormed.view(np.uint32))
+        assert (tok[[0, 5]] < [100, 10]).all()
+
+
+def test_workspace_is_reused_safely_across_batch_sizes():
+    x = dev(randn_bits((256, 8000), 57, 3.0, "bfloat16"), "bfloat16")
+    bits = bits_of(x)
+    for B in (1, 64, 2, 256, 3, 256, 1):
+        want = oracle(bits[:B], "bfloat16", 50, 0.9, np.zeros(B, np.float32)).topk_ids
+        assert np.array_equal(fused.topk_fused(x[:B], 50, splits=4).cpu().numpy(), want), B
+
+
+# --- ablation (reference :164-198) --------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("batch", [1, 8])
+def test_the_last_ablation_phase_is_the_production_path(batch, dtype):
+    x = dev(randn_bits((batch, 4000), 58 + batch, 4.0, dtype), dtype)
+    for top_k in (20, 50):
+        got = fused_sampling.probe_phase(x, top_k, 0.9, 7, 0)
+        want = fused_sampling.sample_fused(x, top_k, 0.9, 0, 0, 0)
+        assert torch.equal(got, want)
+
+
+def test_early_ablation_phases_stop_before_the_answer_exists():
+    x = dev(randn_bits((4, 4000), 60, 4.0, "bfloat16"), "bfloat16")
+    full = fused_sampling.probe_phase(x, 50, 0.9, 7, 0)
+    for phase in (1, 2, 3, 4, 5, 6):
+        assert fused_sampling.probe_phase(x, 50, 0.9, phase, 0).shape == full.shape
+    six = fused_sampling.probe_phase(x, 50, 0.9, 6, 0)
+    assert torch.equal(six, x.float().argmax(-1))
+
+
+def test_ablation_rejects_phases_outside_the_pipeline():
+    x = torch.zeros(2, 4000, device="cuda", dtype=torch.bfloat16)
+    for phase in (0, -1, 8):
+        with pytest.raises(RuntimeError):
+            fused_sampling.probe_phase(x, 50, 0.9, phase, 0)
+
+
+# --- Gate A (reference :201-257) -----------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("top_p", [0.9, 0.95, 1.0])
+@pytest.mark.parametrize("top_k", [1, 20, 50, 100])
+def test_gate_a_keep_and_renormed_match_the_oracle_bit_for_bit(top_k, top_p, dtype):
+    bits = randn_bits((64, 151936), 70 + top_k, 4.0, dtype)
+    x = dev(bits, dtype)
+    s = oracle(bits, dtype, top_k, top_p, np.zeros(64, np.float32))
+    _, keep, ren = fused_sampling.stages_fused(x, top_k, top_p, 0, 0, 0)
+    assert np.array_equal(keep.cpu().numpy(), s.keep)
+    assert np.array_equal(ren.cpu().numpy().view(np.uint32), s.renormed.view(np.uint32))
+    assert (ren.cpu().numpy()[~s.keep] == 0).all()
+    # and within the reference's own tolerance of the fp64 restatement
+    _, _, r64, _ = O.stages_f64(bits, dtype, top_k, top_p)
+    assert np.allclose(ren.cpu().numpy(), r64, atol=2e-6, rtol=0)
+
+
+def test_gate_a_renormed_sums_to_one_over_the_nucleus():
+    x = dev(randn_bits((32, 151936), 80, 4.0, "bfloat16"), "bfloat16")
+    for top_p in (0.9, 0.95, 1.0):
+        _, _, ren = fused_sampling.stages_fused(x, 50, top_p, 0, 0, 0)
+        assert torch.allclose(ren.sum(-1), torch.ones(32, device="cuda"), atol=1e-5)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("top_p,expected_kept", [(0.25, 2), (0.5, 4), (0.75, 6), (0.875, 7)])
+def test_gate_a_cut_lands_exactly_on_the_boundary(top_p, expected_kept, dtype):
+    x = torch.full((4, 4000), -30.0, device="cuda", dtype=TORCH_DTYPE[dtype])
+    x[:, :8] = 10.0
+    _, keep, _ = fused_sampling.stages_fused(x, 8, top_p, 0, 0, 0)
+    assert keep.sum(-1).tolist() == [expected_kept] * 4
+
+
+# --- graphs (reference :260-308) -----------------------------------------------------------------
+
+def test_graph_replay_with_explicit_uniforms_tracks_the_u_buffer():
+    bits = randn_bits((8, 4000), 90, 2.0, "bfloat16")
+    x = dev(bits, "bfloat16")
+    u = torch.zeros(8, device="cuda")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            fused.sample_fused_u(x, 50, 0.95, u)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = fused.sample_fused_u(x, 50, 0.95, u)
+    for i in range(16):
+        un = ustream(8, 100 + i)
+        u.copy_(torch.from_numpy(un))
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy(), oracle(bits, "bfloat16", 50, 0.95, un).token_ids)
+        assert torch.equal(out, fused.sample_fused_u(x, 50, 0.95, u))
+
+
+def test_an_explicit_offset_is_still_reproducible():
+    x = dev(randn_bits((8, 4000), 91, 2.0, "bfloat16"), "bfloat16")
+    a = fused_sampling.sample_fused(x, 50, 0.9, 1234, 7, 0)
+    b = fused_sampling.sample_fused(x, 50, 0.9, 1234, 7, 0)
+    c = fused_sampling.sample_fused(x, 50, 0.9, 1234, 8, 0)
+    assert torch.equal(a, b)
+    assert not torch.equal(a, c)
+
+
+def test_floor_probes_return_the_argmax():
+    bits = randn_bits((8, 151936), 92, 3.0, "bfloat16")
+    x = dev(bits, "bfloat16")
+    want = x.float().argmax(-1)
+    assert torch.equal(fused_sampling.probe_scan_rowblock(x), want)
+    for s in (1, 8, 35, 70, 140, 280):
+        assert torch.equal(fused_sampling.probe_scan_split(x, s), want)
+    assert fused_sampling.probe_noop(x).shape == (8,)
+
+
+def test_kernel_attrs_report_every_instantiation_without_spills_in_the_planned_tilings():
+    rows = fused_sampling.kernel_attrs()
+    assert len(rows) >= 20
+    for name, chunks, threads, vgprs, scratch, lds, blocks in rows:
+        assert threads in (256, 512, 1024) and vgprs > 0 and lds > 0 and blocks >= 1

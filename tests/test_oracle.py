@@ -1,0 +1,266 @@
+"""Pins the CPU oracle (oracle/fsamp_oracle.c) before anything is compared with it.
+
+Each check is independent of the oracle's own code: the reference's closed-form cases
+(tests/golden/known_answers.json, cited per case), textbook routines (numpy's stable argsort,
+float64 exp), the published splitmix64 output, invariants the semantics fix (nucleus is a
+non-empty prefix, cutoff monotone in top_p, mass brackets top_p), and an fp64 restatement.
+"""
+
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+from llm_sampling_kernel_amd import workloads as W
+from oracle import oracle as O
+from tests.golden.make_golden import expand
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+KNOWN = json.load(open(os.path.join(HERE, "golden", "known_answers.json")))
+
+
+def as_input(values, dtype):
+    x = np.asarray(expand(values), dtype=np.float32)
+    if dtype == "float32":
+        return x
+    return W.to_bits(x, dtype)
+
+
+def stages(x, dtype, k, p, u=None, **kw):
+    u = np.zeros(x.shape[0], np.float32) if u is None else u
+    return O.sample(x, dtype, k, p, u, return_stages=True, **kw)
+
+
+def randn(shape, seed, scale=1.0):
+    return np.random.Generator(np.random.PCG64(seed)).standard_normal(shape).astype(np.float32) * scale
+
+
+# --- the order key ------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def test_key_order_is_value_order_over_every_16bit_pattern(dtype):
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    vals = O.to_float(bits, dtype)
+    ok = ~np.isnan(vals)
+    bits, vals = bits[ok], vals[ok]
+    keys = O.key16(bits).astype(np.int64)
+    assert keys.min() >= 1, "key 0 is reserved for padding"
+    order = np.argsort(vals, kind="stable")
+    v, k = vals[order], keys[order]
+    # strictly increasing value <=> strictly increasing key; equal value (only +-0) <=> equal key
+    dv, dk = np.diff(v), np.diff(k)
+    assert np.all((dv > 0) == (dk > 0)) and np.all((dv == 0) == (dk == 0))
+    assert O.key16(np.array([0x8000], np.uint16))[0] == O.key16(np.array([0], np.uint16))[0]
+
+
+# --- exp ----------------------------------------------------------------------------------
+
+def test_expf_is_within_one_ulp_of_float64_exp():
+    x = np.concatenate([np.linspace(-86.0, 0.0, 2_000_001, dtype=np.float32),
+                        -np.abs(randn(200_000, 3, 20.0)) - 0.0,
+                        np.array([0.0, -0.0, -1e-30, -1e-7, -0.5, -0.6931472, -85.99], np.float32)])
+    x = x[x >= -86.0]
+    got = O.expf(x).astype(np.float64)
+    want = np.exp(x.astype(np.float64))
+    ulp = np.spacing(want.astype(np.float32)).astype(np.float64)
+    err = np.abs(got - want) / ulp
+    assert err.max() <= 1.0, f"max error {err.max():.3f} ulp at x={x[err.argmax()]}"
+    assert O.expf(np.array([0.0], np.float32))[0] == 1.0
+
+
+def test_expf_flushes_below_minus_86_and_for_neg_inf():
+    y = O.expf(np.array([-86.0001, -100.0, -1e30, -np.inf], np.float32))
+    assert (y == 0).all()
+    assert O.expf(np.array([-86.0], np.float32))[0] > 0
+
+
+# --- splitmix64 ---------------------------------------------------------------------------
+
+def test_splitmix64_matches_its_published_output_sequence():
+    # first outputs of splitmix64 seeded with 1234567 (the generator's reference sequence)
+    assert O.splitmix64_sequence(1234567, 5) == [
+        6457827717110365317, 3203168211198807973, 9817491932198370423,
+        4593380528125082431, 16408922859458223821]
+
+
+def test_rng_uniform_is_a_24bit_uniform_and_varies_with_every_input():
+    u = O.rng_uniform(7, 3, 100_000)
+    assert u.min() >= 0.0 and u.max() < 1.0
+    assert np.all(u * 16777216.0 == np.floor(u * 16777216.0))
+    assert abs(u.mean() - 0.5) < 0.005
+    assert not np.array_equal(O.rng_uniform(7, 3, 64), O.rng_uniform(7, 4, 64))
+    assert not np.array_equal(O.rng_uniform(7, 3, 64), O.rng_uniform(8, 3, 64))
+
+
+# --- the reference's closed-form cases ----------------------------------------------------------
+
+@pytest.mark.parametrize("case", KNOWN, ids=[c["name"] for c in KNOWN])
+def test_known_answers(case):
+    x = as_input(case["logits"], case["dtype"])
+    B = x.shape[0]
+    for u in ([0.0] * B, [0.5] * B, [0.999999] * B):
+        s = stages(x, case["dtype"], case["top_k"], case["top_p"], np.array(u, np.float32))
+        if "cutoff" in case:
+            assert s.cutoff.tolist() == case["cutoff"]
+        if "keep" in case:
+            assert s.keep.tolist() == case["keep"]
+        if "cumsum" in case:
+            assert s.cumsum.tolist() == case["cumsum"]
+        if "cumsum0" in case:
+            assert s.cumsum[:, 0].tolist() == case["cumsum0"]
+        if "topk_ids" in case:
+            assert s.topk_ids.tolist() == case["topk_ids"]
+        if "topk_vals" in case:
+            assert s.topk_vals.tolist() == case["topk_vals"]
+        if "token_any_u" in case:
+            assert s.token_ids.tolist() == case["token_any_u"]
+
+
+# --- selection against a textbook stable sort -----------------------------------------------------
+
+def brute_topk(x, dtype, k):
+    xf = x if dtype == "float32" else O.to_float(x, dtype)
+    xf = np.where(xf == 0, np.float32(0.0), xf)  # -0 == +0, as in a value sort
+    return np.stack([np.argsort(-xf[r], kind="stable")[:k] for r in range(xf.shape[0])])
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16", "float32"])
+@pytest.mark.parametrize("scale", [4.0, 0.05])
+@pytest.mark.parametrize("k", [1, 20, 100, 1024])
+def test_topk_matches_numpy_stable_argsort(dtype, scale, k):
+    x = randn((6, 5000), 11, scale)
+    x[0, ::7] = 0.0
+    x[1, 1::7] = -0.0
+    x[2, :] = 0.0
+    x[3, 100:] = -np.inf
+    xin = x if dtype == "float32" else W.to_bits(x, dtype)
+    s = stages(xin, dtype, k, 0.9)
+    assert np.array_equal(s.topk_ids, brute_topk(xin, dtype, min(k, 5000)))
+
+
+def test_plus_and_minus_zero_tie_and_resolve_by_id():
+    bits = np.array([[0x8000, 0x0000, 0x8000, 0x3F80, 0x0000]], np.uint16)  # -0 +0 -0 1 +0
+    s = stages(bits, "bfloat16", 5, 1.0)
+    assert s.topk_ids.tolist() == [[3, 0, 1, 2, 4]]
+
+
+def test_topk_larger_than_vocab_is_clamped():
+    s = stages(randn((4, 30), 1), "float32", 500, 0.95)
+    assert s.topk_ids.shape == (4, 30)
+
+
+# --- invariants of the cut and the draw -------------------------------------------------------------
+
+def test_nucleus_is_a_non_empty_prefix_and_brackets_top_p():
+    x = randn((32, 2000), 5)
+    s = stages(x, "float32", 100, 0.9)
+    assert (s.cutoff >= 1).all() and s.keep[:, 0].all()
+    assert not (~s.keep[:, :-1] & s.keep[:, 1:]).any()
+    idx = s.cutoff - 1
+    at = s.cumsum[np.arange(32), idx]
+    before = (s.cumsum - s.probs)[np.arange(32), idx]
+    assert (before < np.float32(0.9)).all()
+    dropped = s.cutoff < 100
+    assert (at[dropped] >= np.float32(0.9) - 1e-6).all()
+
+
+def test_cutoff_is_monotone_in_top_p():
+    x = randn((8, 2000), 6)
+    prev = None
+    for p in (0.5, 0.7, 0.9, 0.95, 0.99):
+        c = stages(x, "float32", 100, p).cutoff
+        if prev is not None:
+            assert (c >= prev).all()
+        prev = c
+
+
+@pytest.mark.parametrize("p", [0.5, 0.9, 0.95, 1.0])
+def test_renormed_sums_to_one_and_is_zero_outside(p):
+    s = stages(randn((32, 3000), 7), "float32", 100, p)
+    assert np.allclose(s.renormed.sum(-1), 1.0, atol=1e-6, rtol=0)
+    assert (s.renormed[~s.keep] == 0).all() and (s.renormed[s.keep] > 0).all()
+
+
+def test_top_p_one_keeps_all_and_k_one_is_the_argmax():
+    x = randn((32, 5000), 8)
+    assert (stages(x, "float32", 100, 1.0).cutoff == 100).all()
+    for p in (0.01, 0.5, 1.0):
+        s = stages(x, "float32", 1, p, np.full(32, 0.7, np.float32))
+        assert np.array_equal(s.token_ids, x.argmax(-1)) and (s.renormed == 1.0).all()
+
+
+@pytest.mark.parametrize("scale", [1e3, 1e10, 1e30, 3e38, -1e3, -1e10, -1e30, -3e38])
+def test_extreme_logits_stay_finite(scale):
+    x = np.zeros((4, 128), np.float32) if scale > 0 else np.full((4, 128), scale, np.float32)
+    x[:, 0] = scale if scale > 0 else scale / 2
+    if scale > 0:
+        x[:, 1] = scale / 2
+    s = stages(x, "float32", 64, 0.95)
+    assert np.isfinite(s.renormed).all() and (s.cutoff >= 1).all()
+    assert np.allclose(s.renormed.sum(-1), 1.0, atol=1e-6, rtol=0)
+
+
+def test_neg_inf_tokens_get_zero_mass_and_are_never_drawn():
+    x = np.full((64, 500), -np.inf, np.float32)
+    x[:, :10] = randn((64, 10), 9)
+    for u in np.linspace(0, 0.999999, 17, dtype=np.float32):
+        s = stages(x, "float32", 100, 1.0, np.full(64, u, np.float32))
+        assert (s.token_ids < 10).all()
+        assert (s.renormed[:, 10:] == 0).all()
+
+
+def test_draw_is_the_inverse_cdf_of_renormed():
+    # stratified u: the empirical frequencies equal the renormed masses up to 1/n
+    probs = [0.40, 0.30, 0.15, 0.10, 0.05]
+    n = 20000
+    x = np.tile(np.log(np.array(probs, np.float32)), (n, 1))
+    u = ((np.arange(n) + 0.5) / n).astype(np.float32)
+    s = stages(x, "float32", 5, 1.0, u)
+    rank = (s.topk_ids == s.token_ids[:, None]).argmax(-1)
+    freq = np.bincount(rank, minlength=5) / n
+    assert np.abs(freq - s.renormed[0]).max() <= 2.0 / n
+
+
+def test_validation_mirrors_reference_policy():
+    x = randn((4, 100), 10)
+    with pytest.raises(ValueError, match="NaN"):
+        y = x.copy(); y[2, 7] = np.nan; O.validate(y, "float32")
+    with pytest.raises(ValueError, match=r"\+inf"):
+        y = x.copy(); y[1, 3] = np.inf; O.validate(y, "float32")
+    with pytest.raises(ValueError, match="entirely -inf"):
+        y = x.copy(); y[3, :] = -np.inf; O.validate(y, "float32")
+    y = x.copy(); y[:, 50:] = -np.inf
+    O.validate(y, "float32")
+
+
+# --- fp32 restatement against fp64 -----------------------------------------------------------------
+
+@pytest.mark.parametrize("name", ["C1", "C2_B16_k50", "C3", "C4_k256", "C4_k1024"])
+def test_fp32_stages_track_the_fp64_restatement(name):
+    c = W.case(name)
+    s = O.sample(c.logits, c.dtype, c.top_k, c.top_p, c.u, return_stages=True)
+    p64, c64, r64, cut64 = O.stages_f64(c.logits, c.dtype, c.top_k, c.top_p)
+    # probabilities: a few ulp (relative 1e-6) of the fp64 values
+    rel = np.abs(s.probs - p64) / np.maximum(p64, 1e-30)
+    assert rel[p64 > 1e-30].max() < 1e-6
+    # cutoff: equal except where the fp64 exclusive prefix sits within 1e-6 of top_p
+    excl64 = c64 - p64
+    near = np.abs(excl64 - c.top_p) < 1e-6
+    agree = s.cutoff == cut64
+    assert (agree | near.any(-1)).all()
+    # retained mass Z_p within 1e-5 relative where the cut agrees
+    zp32 = s.cumsum[np.arange(c.batch), s.cutoff - 1].astype(np.float64)
+    zp64 = c64[np.arange(c.batch), cut64 - 1]
+    assert (np.abs(zp32 - zp64)[agree] / zp64[agree]).max() < 1e-5
+
+
+# --- a planted mistake is caught (the checks above are not vacuous) -----------------------------------
+
+def test_an_inclusive_prefix_cut_would_fail_the_closed_forms():
+    # the classic slip: keep i iff c_i < top_p (inclusive) instead of c_i - p_i < top_p
+    x = np.zeros((1, 8), np.float32)
+    s = stages(x, "float32", 8, 0.5)
+    inclusive_keep = s.cumsum < np.float32(0.5)
+    assert inclusive_keep.sum() != 4 and s.cutoff[0] == 4
