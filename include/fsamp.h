@@ -17,10 +17,13 @@
  *
  * Workspace.  Rows are split over `splits` workgroups and the last workgroup of a row to
  * finish merges the row (one launch per call).  That needs `fsamp_workspace_bytes(...)`
- * bytes of device workspace whose first region holds per-row counters: the region must be
- * zero before the first call (fsamp_workspace_init does that on the stream) and every call
- * leaves it zero again.  Calls that share one workspace must not run concurrently.
- * A plan with splits == 1 needs no workspace (size 0, ws may be NULL).
+ * bytes of device workspace laid out as [per-row counters: round_up(128*B, 256) bytes]
+ * [per-split candidates].  The counter region must be zero before a call
+ * (fsamp_workspace_init zeroes the whole buffer on the stream) and every call leaves it zero
+ * again; the candidate region is scratch.  A buffer reused with a larger B must be zeroed
+ * again, because the larger counter region overlaps the old candidates.  Calls that share
+ * one workspace must not run concurrently.  A plan with splits == 1 needs no workspace
+ * (size 0, ws may be NULL).
  */
 #ifndef FSAMP_H
 #define FSAMP_H
@@ -150,6 +153,19 @@ typedef struct fsamp_attr_row {
 
 /* Writes up to max_rows rows; *n_rows receives the number of instantiations. */
 int fsamp_kernel_attrs(fsamp_attr_row* rows, int32_t max_rows, int32_t* n_rows);
+
+/* Lane-layout self-test of the wave64 primitives the kernel is built on (DPP moves, swizzle,
+ * the fixed-order scan and the bitonic network); writes 12*64 uint32 words to `out` (device).
+ * No counterpart in the reference. */
+int fsamp_debug_wave_selftest(uint32_t* out, hipStream_t stream);
+
+/* Tuning aid with no counterpart in the reference: fsamp_sample (explicit u) that also records
+ * the shader clock (s_memtime) at ten fixed points of every workgroup into
+ * trace[workgroup * 16 + i] (device, B*splits*16 int64, pre-filled by the caller). */
+int fsamp_debug_sample_traced(const void* logits, int dtype, int64_t B, int64_t V,
+                              int64_t top_k, double top_p, const float* u, int64_t* out,
+                              void* ws, size_t ws_bytes, int64_t splits_override,
+                              int64_t* trace, hipStream_t stream);
 
 /* Tuning aid with no counterpart in the reference: force the workgroup size (256, 512 or
  * 1024) that later plans use, or 0 for the automatic choice.  Process-wide, not thread-safe;

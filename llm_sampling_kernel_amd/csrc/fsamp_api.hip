@@ -19,33 +19,42 @@ namespace {
 
 size_t round_up(size_t a, size_t b) { return (a + b - 1) / b * b; }
 
+// per-row arrival counters, one 128-byte line each (atomics on one line serialise)
+size_t counter_bytes(int64_t B) { return round_up((size_t)B * TICKET_STRIDE * 4u, 256); }
+
 // Tiling preference forced by fsamp_debug_force_threads (0 = automatic).
 int g_force_threads = 0;
 
-// Split count when the caller does not force one: enough workgroups to cover the 256 CUs at
-// small batch, one workgroup per row once the batch alone fills the machine.
+// Split count when the caller does not force one: enough workgroups to put a few hundred CUs
+// on a small batch, one workgroup per row once the batch alone fills the machine.  Each extra
+// split costs a hand-off (~3 us at B=1) and widens the row merge.
 int auto_splits(int64_t B) {
   if (B >= 128) return 1;
-  const int64_t s = (256 + B - 1) / B;
-  return (int)std::min<int64_t>(32, std::max<int64_t>(1, s));
+  const int64_t s = (128 + B - 1) / B;
+  return (int)std::min<int64_t>(MAX_SPLITS, std::max<int64_t>(1, s));
 }
 
-// Workgroup size for a slice: 256 threads while 16 chunks per thread hold it, 1024 beyond.
-int preferred_threads(int slice) {
-  if (g_force_threads > 0) return g_force_threads;
-  return slice <= 256 * 8 * 16 ? 256 : 1024;
+// Workgroup size for a slice: 256 threads while 16 chunks per thread hold it, then 512 (up
+// to 38 chunks, 8 waves with room for the slice in VGPRs), then 1024;
+// never fewer threads than k (the slice's lower bound ranks one maximum per thread and the
+// candidate sort one candidate per thread).
+int preferred_threads(int slice, int K) {
+  int want = g_force_threads > 0 ? g_force_threads
+             : (slice <= 256 * 8 * 16 ? 256 : (slice <= 512 * 8 * 38 ? 512 : 1024));
+  while (want < K) want *= 2;
+  return want;
 }
 
 // Smallest compiled tiling of the preferred workgroup size that holds `slice` elements; when
 // that size has none large enough, the smallest-capacity tiling of any size (unless forced).
-const KernelEntry* pick_tiling(int slice, int vec) {
-  const int want = preferred_threads(slice);
+const KernelEntry* pick_tiling(int slice, int vec, int K) {
+  const int want = preferred_threads(slice, K);
   const KernelEntry* best = nullptr;
   const KernelEntry* any = nullptr;
   for (int i = 0; i < kNumKernels; ++i) {
     const KernelEntry& e = kKernels[i];
     const int64_t cap = (int64_t)e.threads * e.chunks * 8;
-    if (e.vec != vec || cap < slice) continue;
+    if (e.vec != vec || cap < slice || e.threads < K) continue;
     if (e.threads == want && (best == nullptr || e.chunks < best->chunks)) best = &e;
     if (any == nullptr || cap < (int64_t)any->threads * any->chunks * 8) any = &e;
   }
@@ -70,15 +79,15 @@ int make_plan_impl(const void* logits, int64_t B, int64_t V, int64_t top_k, int6
   const bool vec = ((uintptr_t)logits % 16 == 0) && (V % 8 == 0);
   const int units = (int)((V + 7) / 8);
   int S = splits_override > 0 ? (int)std::min<int64_t>(splits_override, 1 << 20) : auto_splits(B);
-  // the row's last workgroup merges S*K words in LDS
-  S = std::max(1, std::min({S, CAND_CAP / K, units}));
+  // the row's last workgroup merges S*K words in LDS, ranking across at most MAX_SPLITS lists
+  S = std::max(1, std::min({S, CAND_CAP / K, MAX_SPLITS, units}));
   const KernelEntry* e = nullptr;
   int slice = 0;
   for (;;) {
     slice = ((units + S - 1) / S) * 8;
-    e = pick_tiling(slice, vec ? 1 : 0);
+    e = pick_tiling(slice, vec ? 1 : 0, K);
     if (e != nullptr) break;
-    if (S >= CAND_CAP / K || S >= units) return FSAMP_ERR_VOCAB;
+    if (S >= CAND_CAP / K || S >= MAX_SPLITS || S >= units) return FSAMP_ERR_VOCAB;
     ++S;
   }
   S = (int)((V + slice - 1) / slice);  // no empty trailing split
@@ -89,7 +98,7 @@ int make_plan_impl(const void* logits, int64_t B, int64_t V, int64_t top_k, int6
   pl->vec = vec ? 1 : 0;
   pl->reserved = 0;
   pl->workspace_bytes =
-      S > 1 ? round_up((size_t)B * 4u, 256) + (size_t)B * (size_t)S * (size_t)K * 8u : 0u;
+      S > 1 ? counter_bytes(B) + (size_t)B * (size_t)S * (size_t)K * 8u : 0u;
   if (kern) *kern = e;
   return FSAMP_OK;
 }
@@ -103,7 +112,7 @@ __global__ void fill_zero_kernel(uint32_t* p, size_t n) {
 int launch(const void* logits, int dtype, int64_t B, int64_t V, int64_t top_k, double top_p,
            const float* u, uint64_t seed, uint64_t offset, int64_t* out, int64_t* ids,
            uint8_t* keep, float* renormed, int stop, void* ws, size_t ws_bytes,
-           int64_t splits_override, hipStream_t stream) {
+           int64_t splits_override, hipStream_t stream, int64_t* trace = nullptr) {
   int rc = validate(dtype, B, V, top_k);
   if (rc != FSAMP_OK) return rc;
   if (!(top_p > 0.0 && top_p <= 1.0)) return FSAMP_ERR_TOPP;
@@ -126,7 +135,7 @@ int launch(const void* logits, int dtype, int64_t B, int64_t V, int64_t top_k, d
   p.offset = offset;
   p.tickets = static_cast<uint32_t*>(ws);
   p.partials = pl.workspace_bytes > 0
-                   ? reinterpret_cast<uint64_t*>(static_cast<char*>(ws) + round_up((size_t)B * 4u, 256))
+                   ? reinterpret_cast<uint64_t*>(static_cast<char*>(ws) + counter_bytes(B))
                    : nullptr;
   p.B = (int)B;
   p.V = (int)V;
@@ -138,6 +147,7 @@ int launch(const void* logits, int dtype, int64_t B, int64_t V, int64_t top_k, d
   p.is_bf16 = dtype == FSAMP_DTYPE_BF16 ? 1 : 0;
   p.vec = pl.vec;
   p.stop = stop;
+  p.trace = trace;
   void* args[] = {&p};
   const hipError_t err = hipLaunchKernel(e->fn, dim3((unsigned)(B * pl.splits)), dim3(e->threads),
                                          args, 0, stream);
@@ -235,6 +245,15 @@ int fsamp_debug_force_threads(int32_t threads) {
   if (threads != 0 && threads != 256 && threads != 512 && threads != 1024) return FSAMP_ERR_SHAPE;
   g_force_threads = threads;
   return FSAMP_OK;
+}
+
+int fsamp_debug_sample_traced(const void* logits, int dtype, int64_t B, int64_t V,
+                               int64_t top_k, double top_p, const float* u, int64_t* out,
+                               void* ws, size_t ws_bytes, int64_t splits_override,
+                               int64_t* trace, hipStream_t stream) {
+  if (out == nullptr || trace == nullptr) return FSAMP_ERR_NULL;
+  return launch(logits, dtype, B, V, top_k, top_p, u, 0, 0, out, nullptr, nullptr, nullptr, 7,
+                ws, ws_bytes, splits_override, stream, trace);
 }
 
 int fsamp_kernel_attrs(fsamp_attr_row* rows, int32_t max_rows, int32_t* n_rows) {

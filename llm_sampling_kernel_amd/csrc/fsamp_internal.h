@@ -9,6 +9,8 @@ namespace fsamp {
 constexpr int CAND_CAP = 4096;   // LDS candidate words per workgroup (32 KiB)
 constexpr int NSUB = 8;          // LDS sub-histograms in the radix fallback
 constexpr int RMAX = (FSAMP_K_MAX + 63) / 64;  // ranks per lane in the tail
+constexpr int MAX_SPLITS = 16;  // workgroups per row (the row merge ranks across <= 16 lists)
+constexpr int TICKET_STRIDE = 32;  // u32 words between row counters: one 128-byte line each
 
 // Kernel arguments (passed by value as kernarg).
 struct Params {
@@ -28,6 +30,7 @@ struct Params {
   int is_bf16;
   int vec;                 // rows are 16-byte aligned: dwordx4 loads
   int stop;                // ablation phase (7 = the whole pipeline)
+  int64_t* trace;          // per-workgroup phase timestamps (s_memtime) or nullptr
 };
 
 struct KernelEntry {
@@ -42,7 +45,7 @@ struct KernelEntry {
 // Vector-load (16-byte aligned rows) tilings:
 #define FSAMP_KERNEL_LIST_VEC(X) \
   X(256, 1) X(256, 2) X(256, 3) X(256, 4) X(256, 5) X(256, 6) X(256, 8) X(256, 12) X(256, 16) \
-  X(512, 20) X(512, 24) X(512, 32) X(512, 38) \
+  X(512, 8) X(512, 12) X(512, 16) X(512, 20) X(512, 24) X(512, 32) X(512, 38) \
   X(1024, 4) X(1024, 5) X(1024, 6) X(1024, 8) X(1024, 10) X(1024, 12) X(1024, 16) X(1024, 19)
 // Element-load tilings (rows not 16-byte aligned, V % 8 != 0): small slices only; the planner
 // adds splits until a slice fits.

@@ -16,21 +16,23 @@
 //   key -> value decode                  csrc/fused_sampling.cuh:50-63
 //   splitmix64 uniform                   csrc/fused_sampling.cuh:65-71
 //
-// Selection, MI355X-first:
+// Selection, MI355X-first (one HBM read; every later step works on registers and LDS):
 //   1. every thread issues all of its dwordx4 loads at once (CH chunks of 8 elements, chunk c
-//      of thread t at uint4 index c*NT + t: coalesced), converts them to packed u16 keys with
-//      16-bit packed integer ops and keeps a running packed max (v_pk_max_u16);
-//   2. L = the k-th largest of the NT per-thread maxima is a lower bound of the slice's k-th
-//      largest key (k threads each own an element >= L), found with two 8-bit LDS histograms
-//      over NT values only;
-//   3. elements >= L (typically ~1.5k of them, never the bulk of the slice) are compacted into
-//      LDS as u64 (key << 32 | ~id) words, which are unique, so sorting them orders by value
-//      and then by ascending id: the tie rule needs no extra pass;
-//   4. if more than CAND_CAP elements are >= L (heavy ties), an exact radix select runs over
-//      the register-resident keys instead: two 8-bit LDS histograms (restricted to keys >= L),
-//      a gather of keys above the threshold and an id-ordered block scan of the tied keys that
-//      takes the lowest `need` ids.
-// No pass re-reads HBM.
+//      of thread t at uint4 index c*NT + t: coalesced) and, as each chunk lands, converts it
+//      to packed u16 order keys with 16-bit packed integer ops, keeping the chunk maxima
+//      (two per VGPR) and the thread maximum;
+//   2. L, a lower bound of the slice's k-th largest key: each wave sorts its 64 thread maxima
+//      with a DPP bitonic network, publishes its top ceil(k/W), and the k-th largest of those
+//      W lists (ranked by binary search) owns k distinct elements >= L;
+//   3. elements >= L (typically ~1-2 per qualifying thread) are gathered into per-wave LDS
+//      regions as u64 (key << 32 | ~id) words -- unique, so ordering them orders by value and
+//      then by ascending id, which is the tie rule -- with one compare per chunk (cached maxima);
+//   4. the candidates are ranked by counting (one barrier) into the sorted top-k; if there
+//      are more than one per thread (heavy ties), an exact radix select over the registers
+//      (two 8-bit LDS histograms restricted to keys >= L, a gather above the threshold and an
+//      id-ordered block scan of the tied keys) first reduces them to exactly k.
+// No step re-reads HBM.  Rows split over several workgroups hand their sorted top-k to the
+// row's last workgroup through write-through atomics and are merged by rank.
 
 #include <hip/hip_runtime.h>
 
@@ -38,6 +40,7 @@
 
 #include "fsamp.h"
 #include "fsamp_internal.h"
+#include "fsamp_wave.h"
 
 namespace fsamp {
 
@@ -115,43 +118,85 @@ __device__ __forceinline__ float rng_uniform(uint64_t seed, uint64_t offset, uin
 
 // ---- LDS layout ----------------------------------------------------------------------------
 
+constexpr int STAGE_SLOTS = 2;  // chunk pairs a thread can stage for the gather
+
+template <int NT>
 struct Smem {
-  uint64_t cand[CAND_CAP];   // candidate (key, ~id) words
-  uint32_t hist[NSUB * 256]; // radix histograms (NSUB sub-histograms to spread LDS atomics)
-  uint32_t suf[256];         // suffix sums of the folded histogram
-  int32_t wsum[2][16];       // per-wave partials for block scans (double-buffered)
+  union {
+    uint64_t cand[CAND_CAP];   // radix-select candidates; later the row's split lists
+    struct {
+      uint4 a[STAGE_SLOTS][NT];  // staged chunk pairs: even chunk
+      uint4 b[STAGE_SLOTS][NT];  //                     odd chunk
+    } st;
+  } g;
+  uint64_t top[FSAMP_K_MAX];   // gathered candidates, then the sorted top-K of the slice/row
+  uint8_t meta[STAGE_SLOTS][NT];  // pair index of each staged pair
+  union {
+    struct {
+      uint32_t hist[NSUB * 256];  // radix-fallback histograms (NSUB sub-histograms)
+      uint32_t suf[256];          // suffix sums of the folded histogram
+    } rx;
+    uint32_t lb[1024];            // per-wave sorted thread maxima (lower bound)
+  } u;
+  int32_t wsum[2][16];         // per-wave partials for block scans (double-buffered)
   int32_t misc[16];
 };
 
-enum { M_HB = 0, M_ABOVE, M_LB, M_GT, M_CNT, M_LAST, M_RED, M_TOTAL };
+enum { M_HB = 0, M_ABOVE, M_LB, M_GT, M_CNT, M_RED };
 
 // ---- block primitives ----------------------------------------------------------------------
 
-// inclusive prefix over the first W lanes of the wave (W a power of two <= 64)
-template <int W = 64>
-__device__ __forceinline__ int wave_incl_scan(int v) {
-  const int lane = threadIdx.x & 63;
+// LDS atomics that many lanes aim at one address serialise.  Here each distinct bin among the
+// active lanes of the wave gets one atomicAdd carrying the lane count (the radix fallback runs
+// on tie-heavy data, where most lanes share a bin).
+__device__ __forceinline__ void wave_add(uint32_t* base, uint32_t bin, bool active) {
+  uint64_t todo = __ballot(active);
+  while (todo != 0ull) {
+    const int leader = __builtin_ctzll(todo);
+    const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)bin, leader);
+    const uint64_t same = __ballot(active && bin == b);
+    if (lane_id() == leader) atomicAdd(&base[b], (uint32_t)__popcll(same));
+    todo &= ~same;
+  }
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, xor_lane<1>(v));
+  v = max(v, xor_lane<2>(v));
+  v = max(v, xor_lane<4>(v));
+  v = max(v, xor_lane<8>(v));
+  v = max(v, xor_lane<16>(v));
+  return max(v, xor_lane<32>(v));
+}
+
+// inclusive prefix over the 64 lanes (integers: the association does not matter)
+__device__ __forceinline__ int wave_incl_scan_i32(int v) {
+  const int lane = lane_id();
 #pragma unroll
-  for (int d = 1; d < W; d <<= 1) {
+  for (int d = 1; d < 64; d <<= 1) {
     const int o = __shfl_up(v, d, 64);
     if (lane >= d) v += o;
   }
   return v;
 }
 
-// Exclusive prefix of v over the workgroup in thread order; *total gets the sum.  Each wave
-// scans the per-wave totals itself, so no more than two extra values stay live.
+// Exclusive prefix of v over the workgroup in thread order; *total gets the sum.
 template <int NT>
 __device__ __forceinline__ int block_excl_scan(int v, int* total, int32_t* wsum) {
   constexpr int NW = NT / 64;
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const int incl = wave_incl_scan(v);
+  const int lane = lane_id(), wid = threadIdx.x >> 6;
+  const int incl = wave_incl_scan_i32(v);
   if (lane == 63) wsum[wid] = incl;
   __syncthreads();
-  const int ws = lane < NW ? wsum[lane] : 0;
-  const int wincl = wave_incl_scan<NW>(ws);
-  *total = __shfl(wincl, NW - 1, 64);
-  return __shfl(wincl - ws, wid, 64) + incl - v;
+  int pre = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    const int s = wsum[w];
+    pre += (w < wid) ? s : 0;
+    tot += s;
+  }
+  *total = tot;
+  return pre + incl - v;
 }
 
 // suf[b] = sum of hist[b'] for b' >= b, computed by wave 0; the caller synchronises after.
@@ -164,12 +209,7 @@ __device__ __forceinline__ void suffix256(const uint32_t* hist, uint32_t* suf) {
       h[j] = hist[255 - (4 * l + j)];
       s += h[j];
     }
-    uint32_t incl = s;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const uint32_t o = __shfl_up(incl, d, 64);
-      if (l >= d) incl += o;
-    }
+    const uint32_t incl = (uint32_t)wave_incl_scan_i32((int)s);
     uint32_t run = incl - s;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -209,130 +249,175 @@ __device__ __forceinline__ void zero_hist(uint32_t* hist) {
   for (int i = threadIdx.x; i < NSUB * 256; i += NT) hist[i] = 0u;
 }
 
-// The want-th largest of one 16-bit value per thread (want <= NT), by two 8-bit histograms.
+// Top-K of C unique words in cand[] (C <= NT), written to out[0..min(K, C)) in descending
+// order: each thread ranks one word by counting the words above it (LDS broadcast reads).
 template <int NT>
-__device__ uint32_t block_kth_of_one(uint32_t v, int want, Smem& sm) {
-  zero_hist<NT>(sm.hist);
-  __syncthreads();
-  atomicAdd(&sm.hist[v >> 8], 1u);
-  __syncthreads();
-  suffix256(sm.hist, sm.suf);
-  __syncthreads();
-  find_bucket<NT>(sm.suf, want, 0, &sm.misc[M_HB], &sm.misc[M_ABOVE]);
-  zero_hist<NT>(sm.hist);
-  __syncthreads();
-  const int hb = sm.misc[M_HB];
-  const int above = sm.misc[M_ABOVE];
-  if ((int)(v >> 8) == hb) atomicAdd(&sm.hist[v & 255u], 1u);
-  __syncthreads();
-  suffix256(sm.hist, sm.suf);
-  __syncthreads();
-  find_bucket<NT>(sm.suf, want - above, above, &sm.misc[M_LB], &sm.misc[M_GT]);
-  __syncthreads();
-  return ((uint32_t)hb << 8) | (uint32_t)sm.misc[M_LB];
+__device__ __forceinline__ void rank_sort_topk(const uint64_t* cand, int C, int K, uint64_t* out) {
+  const int i = threadIdx.x;
+  if (i < C) {
+    const uint64_t v = cand[i];
+    int r = 0;
+    int j = 0;
+#pragma unroll 2
+    for (; j + 8 <= C; j += 8) {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) r += (int)(cand[j + q] > v);
+    }
+    for (; j < C; ++j) r += (int)(cand[j] > v);
+    if (r < K) out[r] = v;
+  }
 }
 
-// Descending bitonic sort of cand[0..n) in LDS (n <= CAND_CAP), padded with zeros to a
-// power of two; zero is below every real (key >= 1) word.
-template <int NT>
-__device__ void block_sort_desc(uint64_t* cand, int n) {
-  int P = 1;
-  while (P < n) P <<= 1;
-  for (int i = n + threadIdx.x; i < P; i += NT) cand[i] = 0ull;
-  __syncthreads();
-  for (int k = 2; k <= P; k <<= 1) {
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      for (int q = threadIdx.x; q < (P >> 1); q += NT) {
-        const int i = ((q & ~(j - 1)) << 1) | (q & (j - 1));
-        const int ixj = i + j;
-        const uint64_t a = cand[i], b = cand[ixj];
-        const bool desc = (i & k) == 0;
-        if (desc ? (a < b) : (a > b)) {
-          cand[i] = b;
-          cand[ixj] = a;
-        }
-      }
-      __syncthreads();
+// ---- wave-0 selection helpers ------------------------------------------------------------------
+
+constexpr int WSORT_MAX = 256;  // candidates wave 0 sorts in registers (4 words per lane)
+
+// Wave 0: sort the n <= 64*R words of src[] (zero-padded) and store the top `keep` of them to
+// dst[] in descending order.
+template <int R>
+__device__ __forceinline__ void wave_sort_store(const uint64_t* src, int n, int keep,
+                                                uint64_t* dst) {
+  const int l = lane_id();
+  uint64_t v[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const int e = l * R + i;
+    v[i] = e < n ? src[e] : 0ull;
+  }
+  wave_sort_desc_n<R>(v);
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const int e = l * R + i;
+    if (e < keep) dst[e] = v[i];
+  }
+}
+
+__device__ __forceinline__ void wave_sort_topk(const uint64_t* src, int n, int keep,
+                                               uint64_t* dst) {
+  if (n <= 64) wave_sort_store<1>(src, n, keep, dst);
+  else if (n <= 128) wave_sort_store<2>(src, n, keep, dst);
+  else wave_sort_store<4>(src, n, keep, dst);
+}
+
+// Wave 0: the k-th largest (1-based) of the n <= 64*R unique words of src[].
+template <int R>
+__device__ __forceinline__ uint32_t wave_kth_u32(const uint32_t* src, int n, int k) {
+  const int l = lane_id();
+  if constexpr (R == 1) {
+    const uint32_t w = wave_sort_desc<uint32_t>(l < n ? src[l] : 0u);
+    return read_lane_u32(w, k - 1);
+  }
+  uint64_t v[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const int e = l * R + i;
+    v[i] = e < n ? (uint64_t)src[e] : 0ull;
+  }
+  wave_sort_desc_n<R>(v);
+  const int e = k - 1;
+  uint32_t mine = 0;
+#pragma unroll
+  for (int i = 0; i < R; ++i)
+    if (l * R + i == e) mine = (uint32_t)v[i];
+  return read_lane_u32(mine, e / R);
+}
+
+// Wave 0: merge S descending lists of K words (lists[s*K + i] in LDS, padded with zeros to
+// 64*R) into the descending top K, stored to dst[]: list 0 is loaded in order, every further
+// list reversed across the lanes and folded in with the bitonic top-merge.
+template <int R>
+__device__ __forceinline__ void wave_merge_lists(const uint64_t* lists, int S, int K,
+                                                 uint64_t* dst) {
+  const int l = lane_id();
+  uint64_t a[R], b[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const int f = l * R + i;
+    a[i] = f < K ? lists[f] : 0ull;
+  }
+  for (int s = 1; s < S; ++s) {
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      const int e = 64 * R - 1 - (l * R + i);
+      b[i] = e < K ? lists[s * K + e] : 0ull;
     }
+    wave_merge_top<R>(a, b);
+  }
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const int e = l * R + i;
+    if (e < K) dst[e] = a[i];
   }
 }
 
 // ---- the fp32 tail (one wave) ----------------------------------------------------------------
 
-// Runs on wave 0 with the row's top K words sorted descending in cand[0..K).  The reduction
-// and scan orders are fixed functions of K (R = ceil(K/64) ranks per lane, butterfly and
-// Kogge-Stone over lane distances 1..32) and are mirrored by the CPU oracle.
-__device__ void sample_tail(const Params& p, const uint64_t* cand, int K, int row) {
-  const int l = threadIdx.x;  // 0..63
+// Runs on wave 0 with the row's top K words sorted descending in top[0..K).  Lane l owns
+// ranks [l*R, l*R+R), R = ceil(K/64); per-lane sums are serial, lane values are combined by
+// wave_incl_scan_f32's fixed association (z = its last lane; the prefix offset of lane l =
+// its value at lane l-1).  The CPU oracle evaluates the same operations in the same order.
+// RB >= R bounds the unrolled per-lane loops.
+template <int RB>
+__device__ void sample_tail(const Params& p, const uint64_t* top, int K, int row, float u) {
+  const int l = lane_id();
   const int R = (K + 63) >> 6;
   const int base = l * R;
-  float w[RMAX], pr[RMAX], c[RMAX];
-  const float m = key_to_float((uint32_t)(cand[0] >> 32), p.is_bf16);
+  float w[RB], pr[RB], c[RB];
+  const float m = key_to_float((uint32_t)(top[0] >> 32), p.is_bf16);
   float s = 0.0f;
 #pragma unroll
-  for (int j = 0; j < RMAX; ++j) {
+  for (int j = 0; j < RB; ++j) {
     w[j] = 0.0f;
     if (j < R && base + j < K) {
-      const float x = key_to_float((uint32_t)(cand[base + j] >> 32), p.is_bf16);
+      const float x = key_to_float((uint32_t)(top[base + j] >> 32), p.is_bf16);
       w[j] = exp_nonpos(x - m);
       s = s + w[j];
     }
   }
+  const float z = read_lane_f32(wave_incl_scan_f32(s), 63);
+  float tsum = 0.0f;
 #pragma unroll
-  for (int d = 1; d < 64; d <<= 1) s = s + __shfl_xor(s, d, 64);
-  const float z = s;
-  float t = 0.0f;
-#pragma unroll
-  for (int j = 0; j < RMAX; ++j) {
+  for (int j = 0; j < RB; ++j) {
     pr[j] = 0.0f;
     if (j < R && base + j < K) {
       pr[j] = w[j] / z;
-      t = t + pr[j];
+      tsum = tsum + pr[j];
     }
   }
-  float incl = t;
+  float acc = wave_shr1_f32(wave_incl_scan_f32(tsum));
+  int my_drop = K;
 #pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const float o = __shfl_up(incl, d, 64);
-    if (l >= d) incl = o + incl;
-  }
-  float acc = __shfl_up(incl, 1, 64);
-  if (l == 0) acc = 0.0f;
-  int first_drop = K;
-#pragma unroll
-  for (int j = 0; j < RMAX; ++j) {
+  for (int j = 0; j < RB; ++j) {
     c[j] = 0.0f;
     if (j < R && base + j < K) {
       acc = acc + pr[j];
       c[j] = acc;
       const int idx = base + j;
-      if (idx >= 1 && first_drop == K && !((c[j] - pr[j]) < p.top_p_f)) first_drop = idx;
+      if (idx >= 1 && my_drop == K && !((c[j] - pr[j]) < p.top_p_f)) my_drop = idx;
     }
   }
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) first_drop = min(first_drop, __shfl_xor(first_drop, d, 64));
+  // lanes hold consecutive rank ranges, so the lowest lane with a hit has the first hit
+  const uint64_t drops = __ballot(my_drop < K);
+  const int first_drop = drops ? __builtin_amdgcn_readlane(my_drop, __builtin_ctzll(drops)) : K;
   const int r = (p.keep_all || first_drop == K) ? K - 1 : first_drop - 1;
-  // Z_p = c_r from the lane that owns rank r
   float mine_c = 0.0f;
 #pragma unroll
-  for (int j = 0; j < RMAX; ++j)
+  for (int j = 0; j < RB; ++j)
     if (j == r - base) mine_c = c[j];
-  const float zp = __shfl(mine_c, r / R, 64);
-  const float u = p.u ? p.u[row] : rng_uniform(p.seed, p.offset, (uint32_t)row);
+  const float zp = read_lane_f32(mine_c, r / R);
   const float target = u * zp;
-  int pick = K;
+  int my_pick = K;
 #pragma unroll
-  for (int j = 0; j < RMAX; ++j) {
+  for (int j = 0; j < RB; ++j) {
     const int idx = base + j;
-    if (j < R && idx <= r && pick == K && c[j] >= target) pick = idx;
+    if (j < R && idx <= r && my_pick == K && c[j] >= target) my_pick = idx;
   }
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) pick = min(pick, __shfl_xor(pick, d, 64));
-  if (pick == K) pick = r;
-  if (l == 0) p.out[row] = (int64_t)unpack_id(cand[pick]);
+  const uint64_t hits = __ballot(my_pick < K);
+  const int pick = hits ? __builtin_amdgcn_readlane(my_pick, __builtin_ctzll(hits)) : r;
+  if (l == 0) p.out[row] = (int64_t)unpack_id(top[pick]);
   if (p.keep != nullptr) {
 #pragma unroll
-    for (int j = 0; j < RMAX; ++j) {
+    for (int j = 0; j < RB; ++j) {
       const int idx = base + j;
       if (j < R && idx < K) {
         p.keep[(size_t)row * K + idx] = (uint8_t)(idx <= r);
@@ -342,11 +427,19 @@ __device__ void sample_tail(const Params& p, const uint64_t* cand, int K, int ro
   }
 }
 
+__device__ __forceinline__ void run_tail(const Params& p, const uint64_t* top, int K, int row,
+                                         float u) {
+  if (K <= 64) sample_tail<1>(p, top, K, row, u);
+  else if (K <= 128) sample_tail<2>(p, top, K, row, u);
+  else if (K <= 256) sample_tail<4>(p, top, K, row, u);
+  else if (K <= 512) sample_tail<8>(p, top, K, row, u);
+  else sample_tail<RMAX>(p, top, K, row, u);
+}
+
 // ---- the kernel ----------------------------------------------------------------------------
 
 // Opaque to the optimiser: the keys are "redefined" here, so per-chunk values derived from
-// them in an earlier pass (chunk maxima, masks) are recomputed instead of being kept live
-// across the pass boundary -- at 19 chunks per thread those would cost ~40 VGPRs.
+// them in an earlier pass (masks) are recomputed instead of being kept live across passes.
 template <int CH>
 __device__ __forceinline__ void pass_barrier(uint32_t (&kv)[CH][4]) {
 #pragma unroll
@@ -385,16 +478,21 @@ __device__ __forceinline__ uint32_t key_at(const uint32_t (&k)[4], int j) {
   return (j & 1) ? (w >> 16) : (w & 0xFFFFu);
 }
 
-// max key of one 8-element chunk (two packed dwords per pk_max step)
-__device__ __forceinline__ uint32_t chunk_max(const uint32_t (&k)[4]) {
-  const uint32_t m2 = pkmax(pkmax(k[0], k[1]), pkmax(k[2], k[3]));
-  return max(m2 & 0xFFFFu, m2 >> 16);
-}
+// Phase timestamps for tuning: thread 0 of each workgroup records the shader clock at fixed
+// points into trace[workgroup * 16 + i] when the caller passes a trace buffer.
+#define FSAMP_TRACE(i)                                                                       \
+  do {                                                                                       \
+    if (p.trace != nullptr && threadIdx.x == 0)                                              \
+      p.trace[(size_t)blockIdx.x * 16 + (i)] = (int64_t)__builtin_amdgcn_s_memtime();        \
+  } while (0)
 
 template <int NT, int CH, bool VEC>
 __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
-  __shared__ Smem sm;
+  constexpr int W = NT / 64;          // waves per workgroup
+  constexpr int NP = (CH + 1) / 2;    // chunk pairs
+  __shared__ Smem<NT> sm;
   const int t = threadIdx.x;
+  const int lane = lane_id(), wid = t >> 6;
   const int row = blockIdx.x / p.S;
   const int split = blockIdx.x - row * p.S;
   const uint16_t* xr = p.logits + (size_t)row * (size_t)p.V;
@@ -402,34 +500,43 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
   const int hi = min(lo + p.slice, p.V);
   const int count = max(hi - lo, 0);
   const int keff = min(p.K, count);
+  FSAMP_TRACE(0);
+  // the row's uniform, fetched now so that its latency hides under the slice loads
+  const float u_row = p.u != nullptr ? p.u[row] : rng_uniform(p.seed, p.offset, (uint32_t)row);
+  if (t == 0) sm.misc[M_CNT] = 0;
 
-  // 1. load the slice into registers as packed keys (padding = key 0); thread maximum.
-  //    With VEC, V and the split bounds are multiples of 8, so a chunk is all in or all out.
+  // 1. load the slice into registers as packed keys (padding = key 0).  With VEC, V and the
+  //    split bounds are multiples of 8, so a chunk is all in or all out; chunks past the slice
+  //    load its last vector (a valid address) and are masked, so every load is unconditional
+  //    and the key work on chunk c waits only for chunk c's load.
   uint32_t kv[CH][4];
+  if (count > 0) {
 #pragma unroll
-  for (int c = 0; c < CH; ++c) {
-    const int e0 = lo + (c * NT + t) * 8;
-    if constexpr (VEC) {
-      if (e0 < hi) {
-        const uint4 v = *reinterpret_cast<const uint4*>(xr + e0);
+    for (int c = 0; c < CH; ++c) {
+      const int e0 = lo + (c * NT + t) * 8;
+      if constexpr (VEC) {
+        const uint4 v = *reinterpret_cast<const uint4*>(xr + min(e0, hi - 8));
         kv[c][0] = v.x;
         kv[c][1] = v.y;
         kv[c][2] = v.z;
         kv[c][3] = v.w;
       } else {
-        kv[c][0] = kv[c][1] = kv[c][2] = kv[c][3] = 0u;
-      }
-    } else {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int e = e0 + 2 * q;
-        const uint32_t a = (e < hi) ? (uint32_t)xr[e] : 0u;
-        const uint32_t b = (e + 1 < hi) ? (uint32_t)xr[e + 1] : 0u;
-        kv[c][q] = a | (b << 16);
+        for (int q = 0; q < 4; ++q) {
+          const int e = e0 + 2 * q;
+          const uint32_t a = (e < hi) ? (uint32_t)xr[e] : 0u;
+          const uint32_t b = (e + 1 < hi) ? (uint32_t)xr[e + 1] : 0u;
+          kv[c][q] = a | (b << 16);
+        }
       }
     }
+  } else {
+#pragma unroll
+    for (int c = 0; c < CH; ++c) kv[c][0] = kv[c][1] = kv[c][2] = kv[c][3] = 0u;
   }
-  uint32_t tmax2 = 0;
+  // pm[i]: packed 16-bit maxima over the two chunks of pair i (even halves, odd halves); a
+  // pair holds an element >= X iff pkmax(pm[i], (X-1) in both halves) differs from the latter
+  uint32_t pm[NP];
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     const int e0 = lo + (c * NT + t) * 8;
@@ -444,80 +551,191 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
         if (e + 1 >= hi) k &= 0x0000FFFFu;
       }
       kv[c][q] = k;
-      tmax2 = pkmax(tmax2, k);
     }
+    const uint32_t m2 = pkmax(pkmax(kv[c][0], kv[c][1]), pkmax(kv[c][2], kv[c][3]));
+    pm[c >> 1] = (c & 1) ? pkmax(pm[c >> 1], m2) : m2;
   }
-  const uint32_t tmax = max(tmax2 & 0xFFFFu, tmax2 >> 16);
+  uint32_t tm2 = pm[0];
+#pragma unroll
+  for (int i = 1; i < NP; ++i) tm2 = pkmax(tm2, pm[i]);
+  const uint32_t tmax = max(tm2 & 0xFFFFu, tm2 >> 16);
+  FSAMP_TRACE(1);
+  // pair of chunk c holds an element >= X (X >= 1)
+  auto pair_ge = [&](int c, uint32_t X) -> bool {
+    const uint32_t xm1 = (X - 1u) * 0x10001u;
+    return pkmax(pm[c >> 1], xm1) != xm1;
+  };
 
   if (p.stop == 1) {
+    const uint32_t wmax = wave_max_u32(tmax);
     if (t == 0) sm.misc[M_RED] = 0;
     __syncthreads();
-    atomicMax(&sm.misc[M_RED], (int)tmax);
+    if (lane == 0) atomicMax(&sm.misc[M_RED], (int)wmax);
     __syncthreads();
     if (t == 0 && split == 0) p.out[row] = sm.misc[M_RED];
     return;
   }
 
   int ncand = 0;
+  bool sorted_in_lds = false;
+  const uint64_t* csrc = sm.top;  // where the candidates are
   if (keff > 0) {
-    // 2. lower bound L of the slice's keff-th largest key
-    uint32_t L = 1u;
-    if (keff <= NT) L = max(block_kth_of_one<NT>(tmax, keff, sm), 1u);
+    // 2. lower bound L of the slice's keff-th largest key (keff <= NT by plan): the
+    //    keff-th largest of the union of every wave's top-m thread maxima, m = ceil(keff/W).
+    //    Maxima are made unique by the thread index in the low bits.  Each wave sorts its 64
+    //    maxima with the DPP network and publishes the top m; after one barrier every wave
+    //    sorts the W*m published words itself (no second barrier).  Past 256 published words
+    //    (keff > 256, where the candidates go through the radix select anyway) the looser
+    //    bound min over waves of the wave's m-th maximum is used instead: every wave then has
+    //    m threads, W*m >= keff in all, whose maximum is >= L.  It keeps the register sort of
+    //    more than 256 words out of the phase that still holds the slice in registers.
+    uint32_t L;
+    {
+      const int m = min(64, (keff + W - 1) / W);
+      const int n = W * m;
+      const uint32_t srt = wave_sort_desc<uint32_t>((tmax << 10) | (uint32_t)t);
+      if (n <= WSORT_MAX) {
+        if (lane < m) sm.u.lb[wid * m + lane] = srt;
+      } else {
+        if (lane == m - 1) sm.u.lb[wid] = srt;
+      }
+      __syncthreads();
+      FSAMP_TRACE(2);
+      uint32_t kth;
+      if (n <= 64) {
+        kth = wave_kth_u32<1>(sm.u.lb, n, keff);
+      } else if (n <= 128) {
+        kth = wave_kth_u32<2>(sm.u.lb, n, keff);
+      } else if (n <= WSORT_MAX) {
+        kth = wave_kth_u32<4>(sm.u.lb, n, keff);
+      } else {
+        kth = lane < W ? sm.u.lb[lane] : 0xFFFFFFFFu;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) kth = min(kth, (uint32_t)__shfl_xor((int)kth, d, 64));
+      }
+      L = max(kth >> 10, 1u);
+      FSAMP_TRACE(3);
+    }
     if (p.stop == 2) {
       if (t == 0 && split == 0) p.out[row] = (int64_t)L;
       return;
     }
 
-    // 3. count elements >= L, compact them if they fit.  Per chunk an 8-bit mask of the
-    //    qualifying elements; the rare hits are visited with ffs so that nothing beyond the
-    //    slice's own registers stays live.
-    int mine = 0;
+    // 3. gather the elements >= L into top[] (slots past its capacity are counted, not
+    //    written).  Only threads with a pair >= L hold any, typically one pair each, so one
+    //    pass over the pair maxima stages up to STAGE_SLOTS qualifying pairs per thread in LDS
+    //    (two compares per pair, the pair stored under an exec mask), and the candidates are
+    //    then extracted from the staged copies, where a runtime element index is an address
+    //    instead of a select chain over the register array.  A thread with more qualifying
+    //    pairs than slots gathers from its registers instead (per-chunk branches).
+    {
+      const uint32_t lm1 = (L - 1u) * 0x10001u;
+      int nst = 0;
 #pragma unroll
-    for (int c = 0; c < CH; ++c) {
-      if (chunk_max(kv[c]) >= L) mine += __popc(ge_mask(kv[c], L));
+      for (int i = 0; i < NP; ++i) {
+        const bool hit = pkmax(pm[i], lm1) != lm1;
+        if (hit && nst < STAGE_SLOTS) {
+          sm.g.st.a[nst][t] = make_uint4(kv[2 * i][0], kv[2 * i][1], kv[2 * i][2], kv[2 * i][3]);
+          if (2 * i + 1 < CH)
+            sm.g.st.b[nst][t] = make_uint4(kv[2 * i + 1][0], kv[2 * i + 1][1], kv[2 * i + 1][2],
+                                           kv[2 * i + 1][3]);
+          else
+            sm.g.st.b[nst][t] = make_uint4(0u, 0u, 0u, 0u);
+          sm.meta[nst][t] = (uint8_t)i;
+        }
+        nst += hit ? 1 : 0;
+      }
+      const bool from_regs = nst > STAGE_SLOTS;
+      auto staged_mask = [&](int s) -> uint32_t {
+        const uint4 a = sm.g.st.a[s][t], b = sm.g.st.b[s][t];
+        const uint32_t ka[4] = {a.x, a.y, a.z, a.w}, kb[4] = {b.x, b.y, b.z, b.w};
+        return ge_mask(ka, L) | (ge_mask(kb, L) << 8);
+      };
+      int mine = 0;
+      if (from_regs) {
+#pragma unroll
+        for (int c = 0; c < CH; ++c)
+          if (pair_ge(c, L)) mine += __popc(ge_mask(kv[c], L));
+      } else {
+        for (int s = 0; s < nst; ++s) mine += __popc(staged_mask(s));
+      }
+      FSAMP_TRACE(10);
+      if (__ballot(mine > 0) != 0ull) {
+        const uint32_t incl = wave_incl_scan_u32((uint32_t)mine);
+        int base = 0;
+        if (lane == 63) base = atomicAdd(&sm.misc[M_CNT], (int)incl);
+        int slot = __builtin_amdgcn_readlane(base, 63) + (int)incl - mine;
+        FSAMP_TRACE(11);
+        if (from_regs) {
+#pragma unroll
+          for (int c = 0; c < CH; ++c) {
+            if (pair_ge(c, L)) {
+              uint32_t m = ge_mask(kv[c], L);
+              const uint32_t id0 = (uint32_t)(lo + (c * NT + t) * 8);
+              while (m != 0u) {
+                const int j = __ffs(m) - 1;
+                m &= m - 1u;
+                if (slot < FSAMP_K_MAX) sm.top[slot] = pack(key_at(kv[c], j), id0 + (uint32_t)j);
+                ++slot;
+              }
+            }
+          }
+        } else {
+          for (int s = 0; s < nst; ++s) {
+            uint32_t m = staged_mask(s);
+            const int c0 = 2 * (int)sm.meta[s][t];
+            const uint16_t* ka = reinterpret_cast<const uint16_t*>(&sm.g.st.a[s][t]);
+            const uint16_t* kb = reinterpret_cast<const uint16_t*>(&sm.g.st.b[s][t]);
+            while (m != 0u) {
+              const int j = __ffs(m) - 1;
+              m &= m - 1u;
+              const uint32_t key = j < 8 ? ka[j] : kb[j - 8];
+              const uint32_t id = (uint32_t)(lo + ((c0 + (j >> 3)) * NT + t) * 8 + (j & 7));
+              if (slot < FSAMP_K_MAX) sm.top[slot] = pack(key, id);
+              ++slot;
+            }
+          }
+        }
+      }
+      FSAMP_TRACE(12);
     }
-    int total = 0;
-    const int off = block_excl_scan<NT>(mine, &total, sm.wsum[0]);
-    pass_barrier<CH>(kv);
-    if (total <= CAND_CAP) {
-      int pos = off;
-#pragma unroll
-      for (int c = 0; c < CH; ++c) {
-        if (chunk_max(kv[c]) >= L) {
-          uint32_t m = ge_mask(kv[c], L);
-          const uint32_t id0 = (uint32_t)(lo + (c * NT + t) * 8);
-          while (m != 0u) {
-            const int j = __ffs(m) - 1;
-            m &= m - 1u;
-            sm.cand[pos++] = pack(key_at(kv[c], j), id0 + (uint32_t)j);
-          }
-        }
-      }
-      ncand = total;
-    } else {
-      // 4. exact radix select over the registers (heavy ties): threshold T, keys > T, and the
-      //    lowest-id keys == T in id order
-      const int sub = (t >> 6) & (NSUB - 1);
-      zero_hist<NT>(sm.hist);
+    __syncthreads();
+    FSAMP_TRACE(4);
+    const int total = sm.misc[M_CNT];
+    if (p.stop == 3) {
+      if (t == 0 && split == 0) p.out[row] = total;
+      return;
+    }
+
+    // 4. the slice's top-keff, sorted: up to WSORT_MAX candidates go straight to wave 0's
+    //    register sort below; beyond that (heavy ties) an exact radix select over the
+    //    registers first reduces them to exactly keff.
+    ncand = total;
+    if (total > WSORT_MAX) {
+      // heavy ties: exact radix select over the registers -- threshold T, keys > T, and the
+      // lowest-id keys == T in id order -- into cand[0..keff), then rank them
+      pass_barrier<CH>(kv);
+      const int sub = wid & (NSUB - 1);
+      zero_hist<NT>(sm.u.rx.hist);
       __syncthreads();
 #pragma unroll
       for (int c = 0; c < CH; ++c) {
-        if (chunk_max(kv[c]) >= L) {
+        if (pair_ge(c, L)) {
           uint32_t m = ge_mask(kv[c], L);
           while (m != 0u) {
             const int j = __ffs(m) - 1;
             m &= m - 1u;
-            atomicAdd(&sm.hist[sub * 256 + (key_at(kv[c], j) >> 8)], 1u);
+            wave_add(sm.u.rx.hist + sub * 256, key_at(kv[c], j) >> 8, true);
           }
         }
       }
       __syncthreads();
-      fold_hist<NT>(sm.hist);
+      fold_hist<NT>(sm.u.rx.hist);
       __syncthreads();
-      suffix256(sm.hist, sm.suf);
+      suffix256(sm.u.rx.hist, sm.u.rx.suf);
       __syncthreads();
-      find_bucket<NT>(sm.suf, keff, 0, &sm.misc[M_HB], &sm.misc[M_ABOVE]);
-      zero_hist<NT>(sm.hist);
+      find_bucket<NT>(sm.u.rx.suf, keff, 0, &sm.misc[M_HB], &sm.misc[M_ABOVE]);
+      zero_hist<NT>(sm.u.rx.hist);
       __syncthreads();
       const uint32_t hb = (uint32_t)sm.misc[M_HB];
       const int above = sm.misc[M_ABOVE];
@@ -526,22 +744,22 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
       const uint32_t band_lo = max(hb << 8, L);
 #pragma unroll
       for (int c = 0; c < CH; ++c) {
-        if (chunk_max(kv[c]) >= band_lo) {
+        if (pair_ge(c, band_lo)) {
           uint32_t m = ge_mask(kv[c], band_lo);
           while (m != 0u) {
             const int j = __ffs(m) - 1;
             m &= m - 1u;
             const uint32_t k = key_at(kv[c], j);
-            if ((k >> 8) == hb) atomicAdd(&sm.hist[sub * 256 + (k & 255u)], 1u);
+            wave_add(sm.u.rx.hist + sub * 256, k & 255u, (k >> 8) == hb);
           }
         }
       }
       __syncthreads();
-      fold_hist<NT>(sm.hist);
+      fold_hist<NT>(sm.u.rx.hist);
       __syncthreads();
-      suffix256(sm.hist, sm.suf);
+      suffix256(sm.u.rx.hist, sm.u.rx.suf);
       __syncthreads();
-      find_bucket<NT>(sm.suf, keff - above, above, &sm.misc[M_LB], &sm.misc[M_GT]);
+      find_bucket<NT>(sm.u.rx.suf, keff - above, above, &sm.misc[M_LB], &sm.misc[M_GT]);
       if (t == 0) sm.misc[M_CNT] = 0;
       __syncthreads();
       const uint32_t T = (hb << 8) | (uint32_t)sm.misc[M_LB];
@@ -550,13 +768,13 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
       pass_barrier<CH>(kv);
 #pragma unroll
       for (int c = 0; c < CH; ++c) {
-        if (chunk_max(kv[c]) > T) {
+        if (pair_ge(c, T + 1u)) {
           uint32_t m = ge_mask(kv[c], T + 1u);
           const uint32_t id0 = (uint32_t)(lo + (c * NT + t) * 8);
           while (m != 0u) {
             const int j = __ffs(m) - 1;
             m &= m - 1u;
-            sm.cand[atomicAdd(&sm.misc[M_CNT], 1)] = pack(key_at(kv[c], j), id0 + (uint32_t)j);
+            sm.g.cand[atomicAdd(&sm.misc[M_CNT], 1)] = pack(key_at(kv[c], j), id0 + (uint32_t)j);
           }
         }
       }
@@ -576,62 +794,90 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
           while (tiemask != 0u && rank < need) {
             const int j = __ffs(tiemask) - 1;
             tiemask &= tiemask - 1u;
-            sm.cand[n_gt + rank] = pack(T, id0 + (uint32_t)j);
+            sm.g.cand[n_gt + rank] = pack(T, id0 + (uint32_t)j);
             ++rank;
           }
           taken += chunk_total;
         }
       }
+      __syncthreads();
       ncand = keff;
+      csrc = sm.g.cand;
+      if (keff > WSORT_MAX) {
+        rank_sort_topk<NT>(sm.g.cand, keff, keff, sm.top);
+        sorted_in_lds = true;
+      }
+      __syncthreads();
     }
-    __syncthreads();
-    if (p.stop == 3) {
-      if (t == 0 && split == 0) p.out[row] = ncand;
-      return;
-    }
-    block_sort_desc<NT>(sm.cand, ncand);
   }
+
+  // From here on wave 0 carries the workgroup alone: no more workgroup barriers.
+  if (wid != 0) return;
+  if (keff > 0 && !sorted_in_lds) {
+    wave_sort_topk(csrc, ncand, keff, sm.top);
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  }
+  FSAMP_TRACE(5);
   if (p.stop == 4) {
-    if (t == 0 && split == 0) p.out[row] = keff > 0 ? (int64_t)unpack_id(sm.cand[0]) : -1;
+    if (t == 0 && split == 0) p.out[row] = keff > 0 ? (int64_t)unpack_id(sm.top[0]) : -1;
     return;
   }
 
   if (p.S > 1) {
-    // 5. hand the slice's top-K to the row's last workgroup
+    // 5. hand the slice's sorted top-K to the row's last workgroup.  The words are written
+    //    with agent-scope atomic stores, which write through to the device-coherent level,
+    //    and s_waitcnt(0) holds the wave until every one of them is acknowledged before the
+    //    arrival counter is bumped; the last workgroup reads them back with agent-scope atomic
+    //    loads, which bypass the (per-XCD, non-coherent) L2.  That is the release / acquire
+    //    pair without an L2 writeback or invalidate: on gfx950 a __threadfence costs ~1.5 us
+    //    more per hand-off and the writebacks serialise across workgroups.
     uint64_t* dst = p.partials + ((size_t)row * p.S + split) * p.K;
-    for (int i = t; i < p.K; i += NT) dst[i] = (i < keff) ? sm.cand[i] : 0ull;
-    __threadfence();
-    __syncthreads();
-    if (t == 0) {
-      const unsigned prev = atomicAdd(&p.tickets[row], 1u);
-      sm.misc[M_LAST] = (prev == (unsigned)(p.S - 1)) ? 1 : 0;
-    }
-    __syncthreads();
-    if (sm.misc[M_LAST] == 0) return;
-    __threadfence();
-    if (t == 0) atomicExch(&p.tickets[row], 0u);
+    for (int i = lane; i < p.K; i += 64)
+      __hip_atomic_store(&dst[i], i < keff ? sm.top[i] : 0ull, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);
+    unsigned prev = 0;
+    if (lane == 0)
+      prev = __hip_atomic_fetch_add(&p.tickets[row * TICKET_STRIDE], 1u, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+    prev = read_lane_u32(prev, 0);
+    FSAMP_TRACE(6);
+    if (prev != (unsigned)(p.S - 1)) return;
+    if (lane == 0)
+      __hip_atomic_store(&p.tickets[row * TICKET_STRIDE], 0u, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
     if (p.stop == 5) {
-      if (t == 0) p.out[row] = (int64_t)unpack_id(sm.cand[0]);
+      if (lane == 0) p.out[row] = (int64_t)unpack_id(sm.top[0]);
       return;
     }
-    // 6. merge: the S sorted lists of the row
+    // 6. merge the S sorted lists of the row: stage them in LDS (every load in flight at
+    //    once), then fold them in registers
     const int n = p.S * p.K;
     const uint64_t* src = p.partials + (size_t)row * p.S * p.K;
-    for (int i = t; i < n; i += NT) sm.cand[i] = src[i];
-    __syncthreads();
-    block_sort_desc<NT>(sm.cand, n);
+    for (int i = lane; i < n; i += 64)
+      sm.g.cand[i] = __hip_atomic_load(&src[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    FSAMP_TRACE(7);
+    if (p.K <= 64) wave_merge_lists<1>(sm.g.cand, p.S, p.K, sm.top);
+    else if (p.K <= 128) wave_merge_lists<2>(sm.g.cand, p.S, p.K, sm.top);
+    else if (p.K <= 256) wave_merge_lists<4>(sm.g.cand, p.S, p.K, sm.top);
+    else if (p.K <= 512) wave_merge_lists<8>(sm.g.cand, p.S, p.K, sm.top);
+    else wave_merge_lists<16>(sm.g.cand, p.S, p.K, sm.top);
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    FSAMP_TRACE(8);
   }
   if (p.stop == 5 || p.stop == 6) {
-    if (t == 0) p.out[row] = (int64_t)unpack_id(sm.cand[0]);
+    if (lane == 0) p.out[row] = (int64_t)unpack_id(sm.top[0]);
     return;
   }
 
   // 7. sampling tail, or the candidate ids
   if (p.ids != nullptr) {
-    for (int i = t; i < p.K; i += NT) p.ids[(size_t)row * p.K + i] = (int64_t)unpack_id(sm.cand[i]);
+    for (int i = lane; i < p.K; i += 64) p.ids[(size_t)row * p.K + i] = (int64_t)unpack_id(sm.top[i]);
     return;
   }
-  if (t < 64) sample_tail(p, sm.cand, p.K, row);
+  run_tail(p, sm.top, p.K, row, u_row);
+  FSAMP_TRACE(9);
 }
 
 // ---- instantiation table -----------------------------------------------------------------------

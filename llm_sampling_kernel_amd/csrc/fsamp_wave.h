@@ -1,0 +1,206 @@
+// fsamp_wave.h -- wave64 cross-lane primitives for gfx950 built on DPP, ds_swizzle and
+// ds_bpermute, shared by the sampler kernel and its lane-layout tests.
+//
+// DPP moves (__builtin_amdgcn_update_dpp) are VALU operations with a few cycles of latency;
+// ds_bpermute (what __shfl_* compiles to) round-trips through the LDS crossbar.  The sorting
+// networks and scans here sit on the critical path of a call, so each lane distance uses the
+// cheapest form the hardware has:
+//   xor 1, 2   quad_perm                      xor 8   row_ror:8 (a 16-lane row rotated by 8)
+//   xor 4      row_shl:4 / row_shr:4 + select xor 16  ds_swizzle (bit mode, xor_mask 16)
+//   xor 32     ds_bpermute
+// and the inclusive scan uses row_shr:1,2,4,8 inside 16-lane rows, then row_bcast:15 and
+// row_bcast:31 across rows.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fsamp {
+
+// DPP control words (GFX9 encoding)
+constexpr int DPP_QUAD_XOR1 = 0xB1;  // quad_perm [1,0,3,2]
+constexpr int DPP_QUAD_XOR2 = 0x4E;  // quad_perm [2,3,0,1]
+constexpr int DPP_ROW_SHL4 = 0x104;
+constexpr int DPP_ROW_SHR1 = 0x111;
+constexpr int DPP_ROW_SHR2 = 0x112;
+constexpr int DPP_ROW_SHR4 = 0x114;
+constexpr int DPP_ROW_SHR8 = 0x118;
+constexpr int DPP_ROW_ROR8 = 0x128;
+constexpr int DPP_WAVE_SHR1 = 0x138;
+constexpr int DPP_ROW_BCAST15 = 0x142;
+constexpr int DPP_ROW_BCAST31 = 0x143;
+
+__device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63); }
+
+// value of lane (l ^ J) for J in {1, 2, 4, 8, 16, 32}
+template <int J>
+__device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
+  const int x = (int)v;
+  if constexpr (J == 1) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, x, DPP_QUAD_XOR1, 0xF, 0xF, false);
+  } else if constexpr (J == 2) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, x, DPP_QUAD_XOR2, 0xF, 0xF, false);
+  } else if constexpr (J == 4) {
+    const int up = __builtin_amdgcn_update_dpp(0, x, DPP_ROW_SHL4, 0xF, 0xF, false);
+    const int dn = __builtin_amdgcn_update_dpp(0, x, DPP_ROW_SHR4, 0xF, 0xF, false);
+    return (uint32_t)((lane_id() & 4) ? dn : up);
+  } else if constexpr (J == 8) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, x, DPP_ROW_ROR8, 0xF, 0xF, false);
+  } else if constexpr (J == 16) {
+    return (uint32_t)__builtin_amdgcn_ds_swizzle(x, (16 << 10) | 0x1F);
+  } else {
+    static_assert(J == 32, "lane distance");
+    return (uint32_t)__shfl_xor(x, 32, 64);
+  }
+}
+
+template <int J>
+__device__ __forceinline__ uint64_t xor_lane64(uint64_t v) {
+  const uint32_t lo = xor_lane<J>((uint32_t)v);
+  const uint32_t hi = xor_lane<J>((uint32_t)(v >> 32));
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// One compare-exchange stage of a descending bitonic network over 64 lanes: block size K,
+// partner distance J.  Within a K-block the direction alternates so that the final K=64
+// merge leaves lane 0 with the largest value.
+template <int K, int J, typename T>
+__device__ __forceinline__ T bitonic_step(T v) {
+  T o;
+  if constexpr (sizeof(T) == 8) o = (T)xor_lane64<J>((uint64_t)v);
+  else o = (T)xor_lane<J>((uint32_t)v);
+  const int l = lane_id();
+  const bool desc = (l & K) == 0;
+  const bool lower = (l & J) == 0;
+  const T hi = v > o ? v : o, lo = v > o ? o : v;
+  return (lower == desc) ? hi : lo;
+}
+
+template <int K, int J, typename T>
+__device__ __forceinline__ T bitonic_merge_stages(T v) {
+  v = bitonic_step<K, J>(v);
+  if constexpr (J > 1) v = bitonic_merge_stages<K, J / 2>(v);
+  return v;
+}
+
+template <int K, typename T>
+__device__ __forceinline__ T bitonic_levels(T v) {
+  if constexpr (K > 2) v = bitonic_levels<K / 2>(v);
+  return bitonic_merge_stages<K, K / 2>(v);
+}
+
+// Full descending sort of one value per lane (64 values): lane 0 gets the largest.
+template <typename T>
+__device__ __forceinline__ T wave_sort_desc(T v) {
+  return bitonic_levels<64>(v);
+}
+
+// Inclusive prefix sum over the 64 lanes in a fixed association: Kogge-Stone inside each
+// 16-lane row (distances 1, 2, 4, 8; lane i of a row adds lane i-d when i >= d), then row 1
+// and row 3 add the last lane of the row below (row_bcast:15), then rows 2 and 3 add lane 31
+// (row_bcast:31).  Every add is x_{src} + x_{own} with the source read before the step.
+__device__ __forceinline__ float wave_incl_scan_f32(float v) {
+  int x = __float_as_int(v);
+  x = __float_as_int(__int_as_float(__builtin_amdgcn_update_dpp(0, x, DPP_ROW_SHR1, 0xF, 0xF, true)) + __int_as_float(x));
+  x = __float_as_int(__int_as_float(__builtin_amdgcn_update_dpp(0, x, DPP_ROW_SHR2, 0xF, 0xF, true)) + __int_as_float(x));
+  x = __float_as_int(__int_as_float(__builtin_amdgcn_update_dpp(0, x, DPP_ROW_SHR4, 0xF, 0xF, true)) + __int_as_float(x));
+  x = __float_as_int(__int_as_float(__builtin_amdgcn_update_dpp(0, x, DPP_ROW_SHR8, 0xF, 0xF, true)) + __int_as_float(x));
+  x = __float_as_int(__int_as_float(__builtin_amdgcn_update_dpp(0, x, DPP_ROW_BCAST15, 0xA, 0xF, false)) + __int_as_float(x));
+  x = __float_as_int(__int_as_float(__builtin_amdgcn_update_dpp(0, x, DPP_ROW_BCAST31, 0xC, 0xF, false)) + __int_as_float(x));
+  return __int_as_float(x);
+}
+
+// Value of lane l-1 (0 for lane 0).
+__device__ __forceinline__ float wave_shr1_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), DPP_WAVE_SHR1, 0xF, 0xF, true));
+}
+
+// Uniform value of lane `l` (l uniform).
+__device__ __forceinline__ float read_lane_f32(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+__device__ __forceinline__ uint32_t read_lane_u32(uint32_t v, int l) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, l);
+}
+
+}  // namespace fsamp
+
+namespace fsamp {
+
+// Inclusive prefix sum of unsigned integers over the 64 lanes (same DPP structure as the fp32
+// scan; integer adds, so the association does not matter).
+__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v) {
+  int x = (int)v;
+  x += __builtin_amdgcn_update_dpp(0, x, DPP_ROW_SHR1, 0xF, 0xF, true);
+  x += __builtin_amdgcn_update_dpp(0, x, DPP_ROW_SHR2, 0xF, 0xF, true);
+  x += __builtin_amdgcn_update_dpp(0, x, DPP_ROW_SHR4, 0xF, 0xF, true);
+  x += __builtin_amdgcn_update_dpp(0, x, DPP_ROW_SHR8, 0xF, 0xF, true);
+  x += __builtin_amdgcn_update_dpp(0, x, DPP_ROW_BCAST15, 0xA, 0xF, false);
+  x += __builtin_amdgcn_update_dpp(0, x, DPP_ROW_BCAST31, 0xC, 0xF, false);
+  return (uint32_t)x;
+}
+
+// ---- register sorting networks over 64*R u64 words, blocked layout ------------------------
+// Lane l holds elements e = l*R + i, i < R.  A stage compares e with e ^ J; within a block of
+// K elements the direction is descending when (e & K) == 0, so a full network leaves element 0
+// (lane 0, i = 0) with the largest word.  Distances J < R stay inside a lane; larger ones pair
+// lane l with lane l ^ (J / R).
+
+template <int R, int K, int J>
+__device__ __forceinline__ void net_stage(uint64_t (&v)[R]) {
+  const int l = lane_id();
+  if constexpr (J < R) {
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      if ((i & J) == 0) {
+        const bool desc = (((l * R + i) & K) == 0);
+        const uint64_t a = v[i], b = v[i + J];
+        if ((a < b) == desc) {
+          v[i] = b;
+          v[i + J] = a;
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      const uint64_t o = xor_lane64<J / R>(v[i]);
+      const int e = l * R + i;
+      const bool desc = (e & K) == 0;
+      const bool lower = (e & J) == 0;
+      const uint64_t hi = v[i] > o ? v[i] : o, lo = v[i] > o ? o : v[i];
+      v[i] = (lower == desc) ? hi : lo;
+    }
+  }
+}
+
+template <int R, int K, int J>
+__device__ __forceinline__ void net_merge(uint64_t (&v)[R]) {
+  net_stage<R, K, J>(v);
+  if constexpr (J > 1) net_merge<R, K, J / 2>(v);
+}
+
+template <int R, int K>
+__device__ __forceinline__ void net_sort_levels(uint64_t (&v)[R]) {
+  if constexpr (K > 2) net_sort_levels<R, K / 2>(v);
+  net_merge<R, K, K / 2>(v);
+}
+
+// Full descending sort of the 64*R words.
+template <int R>
+__device__ __forceinline__ void wave_sort_desc_n(uint64_t (&v)[R]) {
+  net_sort_levels<R, 64 * R>(v);
+}
+
+// v holds a descending list A; b_rev holds a descending list B with element e stored at
+// position 64R-1-e.  Leaves v with the descending top 64R of A and B: the elementwise maximum
+// of A and reversed B is a bitonic sequence holding exactly those words; half-cleaners sort it.
+template <int R>
+__device__ __forceinline__ void wave_merge_top(uint64_t (&v)[R], const uint64_t (&b_rev)[R]) {
+#pragma unroll
+  for (int i = 0; i < R; ++i) v[i] = v[i] > b_rev[i] ? v[i] : b_rev[i];
+  net_merge<R, 64 * R, 32 * R>(v);
+}
+
+}  // namespace fsamp

@@ -68,7 +68,7 @@ def make_plan(logits: torch.Tensor, top_k: int, splits_override: int = 0) -> _li
 def _workspace(logits: torch.Tensor, top_k: int, splits_override: int, stream: int):
     """Cached per (device, stream) workspace whose per-row counters are zero.
 
-    Layout (include/fsamp.h): [counters: round_up(4*B, 256) bytes][per-split candidates].
+    Layout (include/fsamp.h): [counters: round_up(128*B, 256) bytes][per-split candidates].
     A call with S > 1 leaves its counters zero and candidates behind them; a later call with a
     larger B would read those candidates as counters, so the buffer is zeroed again whenever
     the counter region grows past what is known to be clean.
@@ -81,7 +81,7 @@ def _workspace(logits: torch.Tensor, top_k: int, splits_override: int, stream: i
         return None, 0
     key = (logits.device.index, stream)
     entry = _WORKSPACES.get(key)
-    counter_bytes = ((4 * B + 255) // 256) * 256
+    counter_bytes = ((128 * B + 255) // 256) * 256
     if entry is None or entry["buf"].numel() < need:
         buf = torch.empty(max(need, 1 << 20), dtype=torch.uint8, device=logits.device)
         _lib.check(lib.fsamp_workspace_init(ctypes.c_void_p(buf.data_ptr()), buf.numel(),

@@ -23,10 +23,12 @@
  * kernel can be compared with it bit for bit:
  *   - exp is oracle_expf() below: Cody-Waite reduction by ln2 plus a degree-7 Taylor polynomial,
  *     evaluated with fmaf; inputs below -86 give exactly 0 (e^-86 < 2^-124);
- *   - the K survivors are dealt to 64 "lanes" in blocks of R = ceil(K/64); z is the sum of
- *     per-lane serial sums combined by a butterfly over lane distances 1,2,4,...,32;
- *   - the prefix c is per-lane serial sums, an inclusive Kogge-Stone scan over lanes with
- *     distances 1,2,...,32, then per-lane serial accumulation from the exclusive offset.
+ *   - the K survivors are dealt to 64 "lanes" in blocks of R = ceil(K/64); per-lane sums are
+ *     serial; the 64 lane values are combined by one fixed inclusive scan (lane_scan below:
+ *     Kogge-Stone over distances 1,2,4,8 inside 16-lane rows, then rows 1 and 3 add the last
+ *     lane of the row below, then rows 2 and 3 add lane 31); z is the scan total of the w
+ *     sums, the prefix c is the exclusive scan offset of the p sums followed by per-lane
+ *     serial accumulation.
  * Against the torch fp32 computation this differs only by rounding; tests pin it against an
  * fp64 restatement (oracle_stages_f64) and the reference's closed-form cases.
  */
@@ -202,37 +204,50 @@ typedef struct {
   int64_t r;     /* last kept rank */
 } tail_out_t;
 
+/* Inclusive prefix of 64 lane values in the sampler's association: Kogge-Stone inside each
+ * 16-lane row (lane i of a row adds lane i-d for d = 1, 2, 4, 8 when i >= d), then rows 1 and
+ * 3 add the last lane of the row below, then rows 2 and 3 add lane 31.  Each step reads the
+ * values of the previous step; every add is (source lane) + (own lane). */
+static void lane_scan(float* v) {
+  float nxt[OR_LANES];
+  for (int d = 1; d < 16; d <<= 1) {
+    for (int l = 0; l < OR_LANES; ++l) nxt[l] = ((l & 15) >= d) ? v[l - d] + v[l] : v[l];
+    memcpy(v, nxt, sizeof(nxt));
+  }
+  for (int l = 0; l < OR_LANES; ++l) {
+    const int row = l >> 4;
+    nxt[l] = (row == 1 || row == 3) ? v[16 * row - 1] + v[l] : v[l];
+  }
+  memcpy(v, nxt, sizeof(nxt));
+  for (int l = 0; l < OR_LANES; ++l) nxt[l] = (l >= 32) ? v[31] + v[l] : v[l];
+  memcpy(v, nxt, sizeof(nxt));
+}
+
 /* x: K candidate values, descending.  Writes w (scratch), p, c; returns r and pick. */
 static tail_out_t tail_f32(const float* x, int K, double top_p, float u, float* w, float* p,
                            float* c) {
   const int R = (K + OR_LANES - 1) / OR_LANES;
-  float lane_s[OR_LANES], nxt[OR_LANES];
+  float lane_s[OR_LANES];
   const float m = x[0];
   for (int j = 0; j < K; ++j) w[j] = oracle_expf(x[j] - m);
 
-  /* z: per-lane serial sums, then a butterfly over lane distances 1..32 */
+  /* z: per-lane serial sums, combined by the lane scan; z is its last lane */
   for (int l = 0; l < OR_LANES; ++l) {
     float s = 0.0f;
     for (int j = l * R; j < l * R + R && j < K; ++j) s = s + w[j];
     lane_s[l] = s;
   }
-  for (int d = 1; d < OR_LANES; d <<= 1) {
-    for (int l = 0; l < OR_LANES; ++l) nxt[l] = lane_s[l] + lane_s[l ^ d];
-    memcpy(lane_s, nxt, sizeof(lane_s));
-  }
-  const float z = lane_s[0];
+  lane_scan(lane_s);
+  const float z = lane_s[OR_LANES - 1];
   for (int j = 0; j < K; ++j) p[j] = w[j] / z;
 
-  /* prefix: per-lane serial totals, inclusive Kogge-Stone scan, exclusive offsets */
+  /* prefix: per-lane serial totals, lane scan, exclusive offsets, serial accumulation */
   for (int l = 0; l < OR_LANES; ++l) {
     float s = 0.0f;
     for (int j = l * R; j < l * R + R && j < K; ++j) s = s + p[j];
     lane_s[l] = s;
   }
-  for (int d = 1; d < OR_LANES; d <<= 1) {
-    for (int l = 0; l < OR_LANES; ++l) nxt[l] = (l >= d) ? lane_s[l - d] + lane_s[l] : lane_s[l];
-    memcpy(lane_s, nxt, sizeof(lane_s));
-  }
+  lane_scan(lane_s);
   for (int l = 0; l < OR_LANES; ++l) {
     float acc = (l == 0) ? 0.0f : lane_s[l - 1];
     for (int j = l * R; j < l * R + R && j < K; ++j) {

@@ -41,17 +41,17 @@ def plan(B, V, k, splits=0, ptr=4096):
 
 
 @pytest.mark.parametrize("B,V,k,S,threads", [
-    (1, 151936, 50, 32, 256),     # C1: 32 splits of 4752 elements
-    (64, 128256, 50, 4, 256),     # C2, B=64
+    (1, 151936, 50, 16, 256),     # C1: 16 splits of 9496 elements
+    (64, 128256, 50, 2, 512),     # C2, B=64: 2 splits of 64128
     (16, 151936, 1024, 4, 1024),  # C4 k=1024: 4 splits, 4096 merged words
-    (256, 151936, 50, 1, 1024),   # C5: one workgroup per row, slice in VGPRs
+    (256, 151936, 50, 1, 512),    # C5: one workgroup per row, slice in VGPRs
 ])
 def test_plans_for_the_benchmark_shapes(B, V, k, S, threads):
     rc, p = plan(B, V, k)
     assert rc == 0 and p.splits == S and p.threads == threads
     assert p.threads * p.chunks * 8 >= p.slice and p.slice * p.splits >= V
     assert p.slice % 8 == 0 and p.vec == 1
-    assert p.workspace_bytes == (0 if S == 1 else ((4 * B + 255) // 256) * 256 + B * S * k * 8)
+    assert p.workspace_bytes == (0 if S == 1 else ((128 * B + 255) // 256) * 256 + B * S * k * 8)
 
 
 def test_every_plan_tiles_its_slice_and_fits_the_merge_buffer():

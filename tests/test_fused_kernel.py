@@ -440,3 +440,22 @@ def test_kernel_attrs_report_every_instantiation_without_spills_in_the_planned_t
     assert len(rows) >= 20
     for name, chunks, threads, vgprs, scratch, lds, blocks in rows:
         assert threads in (256, 512, 1024) and vgprs > 0 and lds > 0 and blocks >= 1
+
+
+def test_wave_primitives_have_the_lane_layouts_the_kernel_assumes():
+    # DPP / swizzle / bpermute moves, the bitonic network and the fixed-order scan
+    out = torch.zeros(12 * 64, dtype=torch.int32, device="cuda")
+    import ctypes
+    _lib.check(_lib.load().fsamp_debug_wave_selftest(ctypes.c_void_p(out.data_ptr()), None))
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().view(np.uint32).reshape(12, 64)
+    lanes = np.arange(64, dtype=np.uint32)
+    for r, j in enumerate((1, 2, 4, 8, 16, 32)):
+        assert np.array_equal(got[r], lanes ^ j), f"xor_lane<{j}>"
+    assert np.array_equal(got[6], 63 - lanes), "wave sort of a permutation"
+    assert np.array_equal(got[7].view(np.float32), ((lanes + 1) * (lanes + 2) / 2).astype(np.float32))
+    assert np.array_equal(got[8].view(np.float32), lanes.astype(np.float32))
+    assert np.array_equal(got[9].view(np.float32), (lanes + 1).astype(np.float32))
+    hi = (lanes * 21) & 63
+    order = np.argsort(-hi.astype(np.int64), kind="stable")
+    assert np.array_equal(got[10], hi[order]) and np.array_equal(got[11], 0xFFFFFFFF - lanes[order])
