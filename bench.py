@@ -118,6 +118,81 @@ def cpu_baseline(case, budget_s: float) -> dict:
             "ms_per_call_c5_equiv": per_call * 1e3 * case.batch / rows}
 
 
+def traffic_probe(calls: int) -> int:
+    """Workload for the HBM-traffic counters: `calls` cold C5 calls, then `calls` plain
+    device-to-device copies of a buffer of the same size (the calibration kernel: it reads and
+    writes exactly B*V*2 bytes).  Run under `rocprofv3 --pmc FETCH_SIZE` and again under
+    `--pmc WRITE_SIZE`; --summarize-traffic turns the two CSVs into the traffic figure."""
+    import torch
+
+    from llm_sampling_kernel_amd import fused
+    from llm_sampling_kernel_amd import workloads as W
+
+    c5 = W.c5()
+    x0 = to_dev(c5.logits, c5.dtype)
+    u5 = torch.from_numpy(c5.u).cuda()
+    bufs = [x0] + [x0.clone() for _ in range(ROTATE - 1)]
+    torch.cuda.synchronize()
+    for i in range(calls):
+        fused.sample_fused_u(bufs[i % ROTATE], c5.top_k, c5.top_p, u5)
+    torch.cuda.synchronize()
+    dst = torch.empty_like(x0)
+    for i in range(calls):
+        dst.copy_(bufs[(i + 7) % ROTATE])
+    torch.cuda.synchronize()
+    log(f"traffic probe: {calls} C5 calls + {calls} copies of {x0.numel() * 2} bytes")
+    return 0
+
+
+def _pmc_means(path: str, counter: str) -> dict:
+    """Mean counter value per dispatch, by kernel family (sampler / copy), from a rocprofv3
+    counter_collection.csv."""
+    import csv
+
+    acc: dict = {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            if r["Counter_Name"] != counter:
+                continue
+            name = r["Kernel_Name"]
+            fam = "sampler" if "fsamp_kernel" in name else ("copy" if "copy" in name.lower()
+                                                             else None)
+            if fam is None:
+                continue
+            acc.setdefault(fam, []).append(float(r["Counter_Value"]))
+    return {k: (sum(v) / len(v), len(v)) for k, v in acc.items()}
+
+
+def summarize_traffic(fetch_csv: str, write_csv: str, out_path: str) -> int:
+    """HBM bytes per sampler launch from the two counter runs, each counter scaled by what it
+    reads for the copy kernel, whose true traffic is B*V*2 bytes read and B*V*2 written."""
+    B, V = 256, 151936
+    copy_bytes = B * V * 2
+    f = _pmc_means(fetch_csv, "FETCH_SIZE")
+    w = _pmc_means(write_csv, "WRITE_SIZE")
+    f_scale = copy_bytes / (f["copy"][0] * 1024.0)
+    w_scale = copy_bytes / (w["copy"][0] * 1024.0)
+    fetch_b = f["sampler"][0] * 1024.0 * f_scale
+    write_b = w["sampler"][0] * 1024.0 * w_scale
+    res = {
+        "kernel": "fsamp_kernel (C5 plan)",
+        "workload": "C5 cold: B=256, V=151936, bf16, k=50, p=0.90, 14 rotated input copies",
+        "fetch_kib_per_dispatch": round(f["sampler"][0], 1),
+        "write_kib_per_dispatch": round(w["sampler"][0], 1),
+        "copy_fetch_kib": round(f["copy"][0], 1), "copy_write_kib": round(w["copy"][0], 1),
+        "copy_bytes": copy_bytes, "fetch_scale": round(f_scale, 4),
+        "write_scale": round(w_scale, 4),
+        "dispatches": {"sampler": f["sampler"][1], "copy": f["copy"][1]},
+        "bytes_per_launch": round(fetch_b + write_b),
+        "algorithmic_bytes": algo_bytes(B, V),
+    }
+    with open(out_path, "w") as fo:
+        json.dump(res, fo, indent=1)
+        fo.write("\n")
+    print(json.dumps(res))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -125,7 +200,15 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--traffic-probe", type=int, metavar="CALLS", default=0,
+                    help="run the workload for the HBM-traffic counters and exit")
+    ap.add_argument("--summarize-traffic", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "OUT"),
+                    help="turn two rocprofv3 counter CSVs into the traffic summary and exit")
     args = ap.parse_args()
+    if args.summarize_traffic:
+        return summarize_traffic(*args.summarize_traffic)
+    if args.traffic_probe:
+        return traffic_probe(args.traffic_probe)
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for "
               f"--gpus {args.gpus}); run with --gpus 1", file=sys.stderr)

@@ -29,18 +29,21 @@ int g_force_threads = 0;
 // on a small batch, one workgroup per row once the batch alone fills the machine.  Each extra
 // split costs a hand-off (~3 us at B=1) and widens the row merge.
 int auto_splits(int64_t B) {
+  // Measured on MI355X (V=151936, k=50): below B=128 a call costs ~11-12 us for any S in 2..6
+  // (the post-load chain and the hand-off dominate, not bandwidth); more splits only add merge
+  // width.  From B=128 on, one workgroup per row already fills half the CUs.
   if (B >= 128) return 1;
-  const int64_t s = (128 + B - 1) / B;
-  return (int)std::min<int64_t>(MAX_SPLITS, std::max<int64_t>(1, s));
+  if (B >= 64) return 2;
+  return 4;
 }
 
-// Workgroup size for a slice: 256 threads while 16 chunks per thread hold it, then 512 (up
-// to 38 chunks, 8 waves with room for the slice in VGPRs), then 1024;
+// Workgroup size for a slice: 256 threads while 8 chunks per thread hold it, then 512 (up to
+// 38 chunks, 8 waves with room for the slice in VGPRs), then 1024;
 // never fewer threads than k (the slice's lower bound ranks one maximum per thread and the
 // candidate sort one candidate per thread).
 int preferred_threads(int slice, int K) {
   int want = g_force_threads > 0 ? g_force_threads
-             : (slice <= 256 * 8 * 16 ? 256 : (slice <= 512 * 8 * 38 ? 512 : 1024));
+             : (slice <= 256 * 8 * 8 ? 256 : (slice <= 512 * 8 * 38 ? 512 : 1024));
   while (want < K) want *= 2;
   return want;
 }

@@ -118,7 +118,7 @@ __device__ __forceinline__ float rng_uniform(uint64_t seed, uint64_t offset, uin
 
 // ---- LDS layout ----------------------------------------------------------------------------
 
-constexpr int STAGE_SLOTS = 2;  // chunk pairs a thread can stage for the gather
+constexpr int STAGE_SLOTS = 4;  // chunk pairs a thread can stage for the gather
 
 template <int NT>
 struct Smem {
@@ -139,6 +139,7 @@ struct Smem {
     uint32_t lb[1024];            // per-wave sorted thread maxima (lower bound)
   } u;
   int32_t wsum[2][16];         // per-wave partials for block scans (double-buffered)
+  int32_t wcnt[16];            // candidates gathered per wave
   int32_t misc[16];
 };
 
@@ -274,15 +275,14 @@ constexpr int WSORT_MAX = 256;  // candidates wave 0 sorts in registers (4 words
 
 // Wave 0: sort the n <= 64*R words of src[] (zero-padded) and store the top `keep` of them to
 // dst[] in descending order.
-template <int R>
-__device__ __forceinline__ void wave_sort_store(const uint64_t* src, int n, int keep,
-                                                uint64_t* dst) {
+template <int R, typename Load>
+__device__ __forceinline__ void wave_sort_store(const Load& src, int n, int keep, uint64_t* dst) {
   const int l = lane_id();
   uint64_t v[R];
 #pragma unroll
   for (int i = 0; i < R; ++i) {
     const int e = l * R + i;
-    v[i] = e < n ? src[e] : 0ull;
+    v[i] = e < n ? src(e) : 0ull;
   }
   wave_sort_desc_n<R>(v);
 #pragma unroll
@@ -292,8 +292,8 @@ __device__ __forceinline__ void wave_sort_store(const uint64_t* src, int n, int 
   }
 }
 
-__device__ __forceinline__ void wave_sort_topk(const uint64_t* src, int n, int keep,
-                                               uint64_t* dst) {
+template <typename Load>
+__device__ __forceinline__ void wave_sort_topk(const Load& src, int n, int keep, uint64_t* dst) {
   if (n <= 64) wave_sort_store<1>(src, n, keep, dst);
   else if (n <= 128) wave_sort_store<2>(src, n, keep, dst);
   else wave_sort_store<4>(src, n, keep, dst);
@@ -323,11 +323,18 @@ __device__ __forceinline__ uint32_t wave_kth_u32(const uint32_t* src, int n, int
 }
 
 // Wave 0: merge S descending lists of K words (lists[s*K + i] in LDS, padded with zeros to
-// 64*R) into the descending top K, stored to dst[]: list 0 is loaded in order, every further
-// list reversed across the lanes and folded in with the bitonic top-merge.
+// 64*R) into the descending top K, left in a[] (element l*R + i in lane l): list 0 is loaded in
+// order, every further list reversed across the lanes and folded in with the bitonic top-merge.
 template <int R>
 __device__ __forceinline__ void wave_merge_lists(const uint64_t* lists, int S, int K,
-                                                 uint64_t* dst) {
+                                                 uint64_t (&a)[R]);
+
+// The same merge with the result stored to dst[0..K).  Wide lists (R = 8, 16) use this form:
+// with the result array owned here the compiler keeps the network within ~100 VGPRs, where
+// passing the caller's array in doubles the register footprint.
+template <int R>
+__device__ __forceinline__ void wave_merge_lists_dst(const uint64_t* lists, int S, int K,
+                                                     uint64_t* dst) {
   const int l = lane_id();
   uint64_t a[R], b[R];
 #pragma unroll
@@ -350,26 +357,52 @@ __device__ __forceinline__ void wave_merge_lists(const uint64_t* lists, int S, i
   }
 }
 
+template <int R>
+__device__ __forceinline__ void wave_merge_lists(const uint64_t* lists, int S, int K,
+                                                 uint64_t (&a)[R]) {
+  const int l = lane_id();
+  uint64_t b[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const int f = l * R + i;
+    a[i] = f < K ? lists[f] : 0ull;
+  }
+  for (int s = 1; s < S; ++s) {
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      const int e = 64 * R - 1 - (l * R + i);
+      b[i] = e < K ? lists[s * K + e] : 0ull;
+    }
+    wave_merge_top<R>(a, b);
+  }
+}
+
 // ---- the fp32 tail (one wave) ----------------------------------------------------------------
 
-// Runs on wave 0 with the row's top K words sorted descending in top[0..K).  Lane l owns
-// ranks [l*R, l*R+R), R = ceil(K/64); per-lane sums are serial, lane values are combined by
-// wave_incl_scan_f32's fixed association (z = its last lane; the prefix offset of lane l =
-// its value at lane l-1).  The CPU oracle evaluates the same operations in the same order.
-// RB >= R bounds the unrolled per-lane loops.
-template <int RB>
-__device__ void sample_tail(const Params& p, const uint64_t* top, int K, int row, float u) {
+// Runs on wave 0 with the row's top K words sorted descending: rank l*R + j, R = ceil(K/64)
+// <= RB, is v[j] of lane l (FROM_LDS false) or top[l*R + j] (FROM_LDS true, for wide K where
+// the words stay in LDS).  Per-lane sums are serial, lane values are combined by
+// wave_incl_scan_f32's fixed association (z = its last lane; the prefix offset of lane l = its
+// value at lane l-1).  The CPU oracle evaluates the same operations in the same order.
+template <int RB, bool FROM_LDS>
+__device__ __forceinline__ void sample_tail(const Params& p, const uint64_t (&v)[RB],
+                                            const uint64_t* top, int K, int row, float u) {
   const int l = lane_id();
   const int R = (K + 63) >> 6;
   const int base = l * R;
+  auto word = [&](int j) -> uint64_t {
+    if constexpr (FROM_LDS) return top[base + j];
+    else return v[j];
+  };
   float w[RB], pr[RB], c[RB];
-  const float m = key_to_float((uint32_t)(top[0] >> 32), p.is_bf16);
+  const float m = FROM_LDS ? key_to_float((uint32_t)(top[0] >> 32), p.is_bf16)
+                           : key_to_float(read_lane_u32((uint32_t)(v[0] >> 32), 0), p.is_bf16);
   float s = 0.0f;
 #pragma unroll
   for (int j = 0; j < RB; ++j) {
     w[j] = 0.0f;
     if (j < R && base + j < K) {
-      const float x = key_to_float((uint32_t)(top[base + j] >> 32), p.is_bf16);
+      const float x = key_to_float((uint32_t)(word(j) >> 32), p.is_bf16);
       w[j] = exp_nonpos(x - m);
       s = s + w[j];
     }
@@ -414,7 +447,19 @@ __device__ void sample_tail(const Params& p, const uint64_t* top, int K, int row
   }
   const uint64_t hits = __ballot(my_pick < K);
   const int pick = hits ? __builtin_amdgcn_readlane(my_pick, __builtin_ctzll(hits)) : r;
-  if (l == 0) p.out[row] = (int64_t)unpack_id(top[pick]);
+  // the picked word: rank pick is v[pick % R] of lane pick / R (both uniform)
+  uint32_t lo32;
+  if constexpr (FROM_LDS) {
+    lo32 = (uint32_t)top[pick];
+  } else {
+    const int pl = pick / R, pj = pick - pl * R;
+    lo32 = 0;
+#pragma unroll
+    for (int j = 0; j < RB; ++j)
+      if (j == pj) lo32 = (uint32_t)v[j];
+    lo32 = read_lane_u32(lo32, pl);
+  }
+  if (l == 0) p.out[row] = (int64_t)(0xFFFFFFFFu - lo32);
   if (p.keep != nullptr) {
 #pragma unroll
     for (int j = 0; j < RB; ++j) {
@@ -427,13 +472,37 @@ __device__ void sample_tail(const Params& p, const uint64_t* top, int K, int row
   }
 }
 
-__device__ __forceinline__ void run_tail(const Params& p, const uint64_t* top, int K, int row,
-                                         float u) {
-  if (K <= 64) sample_tail<1>(p, top, K, row, u);
-  else if (K <= 128) sample_tail<2>(p, top, K, row, u);
-  else if (K <= 256) sample_tail<4>(p, top, K, row, u);
-  else if (K <= 512) sample_tail<8>(p, top, K, row, u);
-  else sample_tail<RMAX>(p, top, K, row, u);
+// Wave 0, after the slice's (or row's) top K words are in v[] blocked by RB (element l*RB + i
+// in lane l, zeros past the end): the candidate ids, or the tail, which needs them blocked by
+// R = ceil(K/64); when R < RB they are re-laid out through top[].
+template <int RB>
+__device__ __forceinline__ void wave_finish(const Params& p, uint64_t (&v)[RB], uint64_t* top, int row,
+                            float u) {
+  const int l = lane_id();
+  const int K = p.K;
+  if (p.ids != nullptr) {
+#pragma unroll
+    for (int i = 0; i < RB; ++i) {
+      const int e = l * RB + i;
+      if (e < K) p.ids[(size_t)row * K + e] = (int64_t)unpack_id(v[i]);
+    }
+    return;
+  }
+  const int R = (K + 63) >> 6;
+  if (R != RB) {
+#pragma unroll
+    for (int i = 0; i < RB; ++i) {
+      const int e = l * RB + i;
+      if (e < K) top[e] = v[i];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+#pragma unroll
+    for (int j = 0; j < RB; ++j) {
+      const int e = l * R + j;
+      v[j] = (j < R && e < K) ? top[e] : 0ull;
+    }
+  }
+  sample_tail<RB, false>(p, v, top, K, row, u);
 }
 
 // ---- the kernel ----------------------------------------------------------------------------
@@ -449,15 +518,20 @@ __device__ __forceinline__ void pass_barrier(uint32_t (&kv)[CH][4]) {
   }
 }
 
-// bit j set when element j (0..7) of the chunk has key >= L
+// bit j set when element j (0..7) of the chunk has key >= L (L >= 1): per word, a saturating
+// packed subtract of L-1 leaves a nonzero half exactly where key >= L, a packed min with 1
+// turns the halves into 0/1, and the low-half bits (2q) and high-half bits (16 + 2q) of the
+// four words are folded into bits 2q and 2q+1.
 __device__ __forceinline__ uint32_t ge_mask(const uint32_t (&k)[4], uint32_t L) {
-  uint32_t m = 0;
+  const u16x2 lm1 = (u16x2)((unsigned short)(L - 1u));
+  const u16x2 one = (u16x2)((unsigned short)1);
+  uint32_t acc = 0;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
-    m |= (uint32_t)((k[q] & 0xFFFFu) >= L) << (2 * q);
-    m |= (uint32_t)((k[q] >> 16) >= L) << (2 * q + 1);
+    const u16x2 d = __builtin_elementwise_sub_sat(__builtin_bit_cast(u16x2, k[q]), lm1);
+    acc |= __builtin_bit_cast(uint32_t, __builtin_elementwise_min(d, one)) << (2 * q);
   }
-  return m;
+  return (acc | (acc >> 15)) & 0xFFu;
 }
 
 // bit j set when element j of the chunk has key == T
@@ -483,13 +557,217 @@ __device__ __forceinline__ uint32_t key_at(const uint32_t (&k)[4], int j) {
 #define FSAMP_TRACE(i)                                                                       \
   do {                                                                                       \
     if (p.trace != nullptr && threadIdx.x == 0)                                              \
-      p.trace[(size_t)blockIdx.x * 16 + (i)] = (int64_t)__builtin_amdgcn_s_memtime();        \
+      p.trace[(size_t)blockIdx.x * 32 + (i)] = (int64_t)__builtin_amdgcn_s_memtime();        \
   } while (0)
+// the constant-rate (100 MHz) clock into slot 16 + i, to convert shader clocks to time
+#define FSAMP_RTRACE(i)                                                                      \
+  do {                                                                                       \
+    if (p.trace != nullptr && threadIdx.x == 0)                                              \
+      p.trace[(size_t)blockIdx.x * 32 + 16 + (i)] =                                          \
+          (int64_t)__builtin_amdgcn_s_memrealtime();                                         \
+  } while (0)
+
+// Wave 0 after the gather.  The slice's top keff words, sorted, go to v[] blocked by RB
+// (element l*RB + i in lane l, zeros past keff): candidates in per-wave regions of top[] or
+// contiguous in cand[] are sorted in registers; sorted_in_lds means top[] already holds them.
+// With S > 1 the list is handed to the row's last workgroup, which merges the S lists; the
+// owner of the row's top K finishes (ids or the sampling tail).
+template <int RB, int NT>
+__device__ __forceinline__ void wave_back_wide(const Params& p, Smem<NT>& sm, int keff, int ncand,
+                                               bool sorted_in_lds, bool regions, int row,
+                                               int split, float u_row);
+
+template <int RB, int NT>
+__device__ __forceinline__ void wave_back(const Params& p, Smem<NT>& sm, int keff, int ncand, bool sorted_in_lds,
+                          bool regions, int row, int split, float u_row) {
+  if constexpr (RB > 4) {
+    wave_back_wide<RB, NT>(p, sm, keff, ncand, sorted_in_lds, regions, row, split, u_row);
+    return;
+  }
+  constexpr int W = NT / 64;
+  constexpr int RW = FSAMP_K_MAX / W;
+  const int l = lane_id();
+  uint64_t v[RB];
+  if (keff > 0 && !sorted_in_lds) {
+    // candidate e: per-wave regions are read through the prefix of the region counts
+    int cnt[W];
+#pragma unroll
+    for (int w = 0; w < W; ++w) cnt[w] = regions ? sm.wcnt[w] : 0;
+    const uint64_t* base = regions ? sm.top : sm.g.cand;
+    auto load = [&](int e) -> uint64_t {
+      int a = e, pre = 0;
+#pragma unroll
+      for (int w = 1; w < W; ++w) {
+        pre += cnt[w - 1];
+        a += (regions && e >= pre) ? RW - cnt[w - 1] : 0;
+      }
+      return base[a];
+    };
+    if (ncand <= 64 * RB) {
+#pragma unroll
+      for (int i = 0; i < RB; ++i) {
+        const int e = l * RB + i;
+        v[i] = e < ncand ? load(e) : 0ull;
+      }
+      FSAMP_TRACE(14);
+      wave_sort_desc_n<RB>(v);
+#pragma unroll
+      for (int i = 0; i < RB; ++i)
+        if (l * RB + i >= keff) v[i] = 0ull;
+    } else {
+      wave_sort_topk(load, ncand, keff, sm.top);
+      sorted_in_lds = true;
+    }
+  }
+  if (keff > 0 && sorted_in_lds) {
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+#pragma unroll
+    for (int i = 0; i < RB; ++i) {
+      const int e = l * RB + i;
+      v[i] = e < keff ? sm.top[e] : 0ull;
+    }
+  }
+  if (keff <= 0) {
+#pragma unroll
+    for (int i = 0; i < RB; ++i) v[i] = 0ull;
+  }
+  FSAMP_TRACE(5);
+  if (p.stop == 4) {
+    if (l == 0 && split == 0) p.out[row] = keff > 0 ? (int64_t)unpack_id(v[0]) : -1;
+    return;
+  }
+
+  if (p.S > 1) {
+    // 5. hand the slice's sorted top-K to the row's last workgroup.  The words are written
+    //    with agent-scope atomic stores, which write through to the device-coherent level,
+    //    and s_waitcnt(0) holds the wave until every one of them is acknowledged before the
+    //    arrival counter is bumped; the last workgroup reads them back with agent-scope atomic
+    //    loads, which bypass the (per-XCD, non-coherent) L2.  That is the release / acquire
+    //    pair without an L2 writeback or invalidate: on gfx950 a __threadfence costs ~1.5 us
+    //    more per hand-off and the writebacks serialise across workgroups.
+    uint64_t* dst = p.partials + ((size_t)row * p.S + split) * p.K;
+#pragma unroll
+    for (int i = 0; i < RB; ++i) {
+      const int e = l * RB + i;
+      if (e < p.K) __hip_atomic_store(&dst[e], v[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    unsigned prev = 0;
+    if (l == 0)
+      prev = __hip_atomic_fetch_add(&p.tickets[row * TICKET_STRIDE], 1u, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+    prev = read_lane_u32(prev, 0);
+    FSAMP_TRACE(6);
+    if (prev != (unsigned)(p.S - 1)) return;
+    if (l == 0)
+      __hip_atomic_store(&p.tickets[row * TICKET_STRIDE], 0u, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    if (p.stop == 5) {
+      if (l == 0) p.out[row] = (int64_t)unpack_id(v[0]);
+      return;
+    }
+    // 6. merge the S sorted lists of the row: stage them in LDS (every load in flight at
+    //    once), then fold them in registers
+    const int n = p.S * p.K;
+    const uint64_t* src = p.partials + (size_t)row * p.S * p.K;
+    for (int i = l; i < n; i += 64)
+      sm.g.cand[i] = __hip_atomic_load(&src[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    FSAMP_TRACE(7);
+    wave_merge_lists<RB>(sm.g.cand, p.S, p.K, v);
+    FSAMP_TRACE(8);
+  }
+  if (p.stop == 5 || p.stop == 6) {
+    if (l == 0) p.out[row] = (int64_t)unpack_id(v[0]);
+    return;
+  }
+  // 7. candidate ids, or the sampling tail
+  wave_finish<RB>(p, v, sm.top, row, u_row);
+  FSAMP_TRACE(9);
+  FSAMP_RTRACE(1);
+}
+
+// Wave 0 for K > 256: the same steps with the sorted words kept in top[] (LDS) between them,
+// so that only the merge holds the wide lists in registers.
+template <int RB, int NT>
+__device__ __forceinline__ void wave_back_wide(const Params& p, Smem<NT>& sm, int keff, int ncand,
+                                               bool sorted_in_lds, bool regions, int row,
+                                               int split, float u_row) {
+  constexpr int W = NT / 64;
+  constexpr int RW = FSAMP_K_MAX / W;
+  const int l = lane_id();
+  if (keff > 0 && !sorted_in_lds) {
+    int cnt[W];
+#pragma unroll
+    for (int w = 0; w < W; ++w) cnt[w] = regions ? sm.wcnt[w] : 0;
+    const uint64_t* base = regions ? sm.top : sm.g.cand;
+    auto load = [&](int e) -> uint64_t {
+      int a = e, pre = 0;
+#pragma unroll
+      for (int w = 1; w < W; ++w) {
+        pre += cnt[w - 1];
+        a += (regions && e >= pre) ? RW - cnt[w - 1] : 0;
+      }
+      return base[a];
+    };
+    wave_sort_topk(load, ncand, keff, sm.top);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  FSAMP_TRACE(5);
+  if (p.stop == 4) {
+    if (l == 0 && split == 0) p.out[row] = keff > 0 ? (int64_t)unpack_id(sm.top[0]) : -1;
+    return;
+  }
+  if (p.S > 1) {
+    // hand-off and merge as in wave_back, through top[]
+    uint64_t* dst = p.partials + ((size_t)row * p.S + split) * p.K;
+    for (int i = l; i < p.K; i += 64)
+      __hip_atomic_store(&dst[i], i < keff ? sm.top[i] : 0ull, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);
+    unsigned prev = 0;
+    if (l == 0)
+      prev = __hip_atomic_fetch_add(&p.tickets[row * TICKET_STRIDE], 1u, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+    prev = read_lane_u32(prev, 0);
+    FSAMP_TRACE(6);
+    if (prev != (unsigned)(p.S - 1)) return;
+    if (l == 0)
+      __hip_atomic_store(&p.tickets[row * TICKET_STRIDE], 0u, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    if (p.stop == 5) {
+      if (l == 0) p.out[row] = (int64_t)unpack_id(sm.top[0]);
+      return;
+    }
+    const int n = p.S * p.K;
+    const uint64_t* src = p.partials + (size_t)row * p.S * p.K;
+    for (int i = l; i < n; i += 64)
+      sm.g.cand[i] = __hip_atomic_load(&src[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    FSAMP_TRACE(7);
+    wave_merge_lists_dst<RB>(sm.g.cand, p.S, p.K, sm.top);
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    FSAMP_TRACE(8);
+  }
+  if (p.stop == 5 || p.stop == 6) {
+    if (l == 0) p.out[row] = (int64_t)unpack_id(sm.top[0]);
+    return;
+  }
+  if (p.ids != nullptr) {
+    for (int i = l; i < p.K; i += 64) p.ids[(size_t)row * p.K + i] = (int64_t)unpack_id(sm.top[i]);
+    return;
+  }
+  const uint64_t none[RB] = {};
+  sample_tail<RB, true>(p, none, sm.top, p.K, row, u_row);
+  FSAMP_TRACE(9);
+  FSAMP_RTRACE(1);
+}
 
 template <int NT, int CH, bool VEC>
 __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
   constexpr int W = NT / 64;          // waves per workgroup
   constexpr int NP = (CH + 1) / 2;    // chunk pairs
+  constexpr int RW = FSAMP_K_MAX / W; // per-wave candidate region in top[]
   __shared__ Smem<NT> sm;
   const int t = threadIdx.x;
   const int lane = lane_id(), wid = t >> 6;
@@ -501,6 +779,7 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
   const int count = max(hi - lo, 0);
   const int keff = min(p.K, count);
   FSAMP_TRACE(0);
+  FSAMP_RTRACE(0);
   // the row's uniform, fetched now so that its latency hides under the slice loads
   const float u_row = p.u != nullptr ? p.u[row] : rng_uniform(p.seed, p.offset, (uint32_t)row);
   if (t == 0) sm.misc[M_CNT] = 0;
@@ -578,7 +857,7 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
 
   int ncand = 0;
   bool sorted_in_lds = false;
-  const uint64_t* csrc = sm.top;  // where the candidates are
+  bool regions = true;  // candidates in per-wave regions of top[] (else contiguous in cand[])
   if (keff > 0) {
     // 2. lower bound L of the slice's keff-th largest key (keff <= NT by plan): the
     //    keff-th largest of the union of every wave's top-m thread maxima, m = ceil(keff/W).
@@ -621,8 +900,8 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
       return;
     }
 
-    // 3. gather the elements >= L into top[] (slots past its capacity are counted, not
-    //    written).  Only threads with a pair >= L hold any, typically one pair each, so one
+    // 3. gather the elements >= L into top[], wave w into top[w*RW, (w+1)*RW) (slots past a
+    //    region are counted, not written; an overfull region sends the slice to the radix path).  Only threads with a pair >= L hold any, typically one pair each, so one
     //    pass over the pair maxima stages up to STAGE_SLOTS qualifying pairs per thread in LDS
     //    (two compares per pair, the pair stored under an exec mask), and the candidates are
     //    then extracted from the staged copies, where a runtime element index is an address
@@ -645,6 +924,7 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
         }
         nst += hit ? 1 : 0;
       }
+      FSAMP_TRACE(13);
       const bool from_regs = nst > STAGE_SLOTS;
       auto staged_mask = [&](int s) -> uint32_t {
         const uint4 a = sm.g.st.a[s][t], b = sm.g.st.b[s][t];
@@ -660,11 +940,12 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
         for (int s = 0; s < nst; ++s) mine += __popc(staged_mask(s));
       }
       FSAMP_TRACE(10);
+      uint32_t wtot = 0;
       if (__ballot(mine > 0) != 0ull) {
         const uint32_t incl = wave_incl_scan_u32((uint32_t)mine);
-        int base = 0;
-        if (lane == 63) base = atomicAdd(&sm.misc[M_CNT], (int)incl);
-        int slot = __builtin_amdgcn_readlane(base, 63) + (int)incl - mine;
+        wtot = read_lane_u32(incl, 63);
+        int slot = (int)incl - mine;
+        uint64_t* region = sm.top + wid * RW;
         FSAMP_TRACE(11);
         if (from_regs) {
 #pragma unroll
@@ -675,7 +956,7 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
               while (m != 0u) {
                 const int j = __ffs(m) - 1;
                 m &= m - 1u;
-                if (slot < FSAMP_K_MAX) sm.top[slot] = pack(key_at(kv[c], j), id0 + (uint32_t)j);
+                if (slot < RW) region[slot] = pack(key_at(kv[c], j), id0 + (uint32_t)j);
                 ++slot;
               }
             }
@@ -691,17 +972,25 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
               m &= m - 1u;
               const uint32_t key = j < 8 ? ka[j] : kb[j - 8];
               const uint32_t id = (uint32_t)(lo + ((c0 + (j >> 3)) * NT + t) * 8 + (j & 7));
-              if (slot < FSAMP_K_MAX) sm.top[slot] = pack(key, id);
+              if (slot < RW) region[slot] = pack(key, id);
               ++slot;
             }
           }
         }
       }
+      if (lane == 0) sm.wcnt[wid] = (int)wtot;
       FSAMP_TRACE(12);
     }
     __syncthreads();
     FSAMP_TRACE(4);
-    const int total = sm.misc[M_CNT];
+    int total = 0;
+    bool wave_over = false;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      const int n = sm.wcnt[w];
+      total += n;
+      wave_over |= n > RW;
+    }
     if (p.stop == 3) {
       if (t == 0 && split == 0) p.out[row] = total;
       return;
@@ -711,7 +1000,7 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
     //    register sort below; beyond that (heavy ties) an exact radix select over the
     //    registers first reduces them to exactly keff.
     ncand = total;
-    if (total > WSORT_MAX) {
+    if (total > WSORT_MAX || wave_over) {
       // heavy ties: exact radix select over the registers -- threshold T, keys > T, and the
       // lowest-id keys == T in id order -- into cand[0..keff), then rank them
       pass_barrier<CH>(kv);
@@ -802,7 +1091,7 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
       }
       __syncthreads();
       ncand = keff;
-      csrc = sm.g.cand;
+      regions = false;
       if (keff > WSORT_MAX) {
         rank_sort_topk<NT>(sm.g.cand, keff, keff, sm.top);
         sorted_in_lds = true;
@@ -813,71 +1102,11 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
 
   // From here on wave 0 carries the workgroup alone: no more workgroup barriers.
   if (wid != 0) return;
-  if (keff > 0 && !sorted_in_lds) {
-    wave_sort_topk(csrc, ncand, keff, sm.top);
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-  }
-  FSAMP_TRACE(5);
-  if (p.stop == 4) {
-    if (t == 0 && split == 0) p.out[row] = keff > 0 ? (int64_t)unpack_id(sm.top[0]) : -1;
-    return;
-  }
-
-  if (p.S > 1) {
-    // 5. hand the slice's sorted top-K to the row's last workgroup.  The words are written
-    //    with agent-scope atomic stores, which write through to the device-coherent level,
-    //    and s_waitcnt(0) holds the wave until every one of them is acknowledged before the
-    //    arrival counter is bumped; the last workgroup reads them back with agent-scope atomic
-    //    loads, which bypass the (per-XCD, non-coherent) L2.  That is the release / acquire
-    //    pair without an L2 writeback or invalidate: on gfx950 a __threadfence costs ~1.5 us
-    //    more per hand-off and the writebacks serialise across workgroups.
-    uint64_t* dst = p.partials + ((size_t)row * p.S + split) * p.K;
-    for (int i = lane; i < p.K; i += 64)
-      __hip_atomic_store(&dst[i], i < keff ? sm.top[i] : 0ull, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_s_waitcnt(0);
-    unsigned prev = 0;
-    if (lane == 0)
-      prev = __hip_atomic_fetch_add(&p.tickets[row * TICKET_STRIDE], 1u, __ATOMIC_RELAXED,
-                                    __HIP_MEMORY_SCOPE_AGENT);
-    prev = read_lane_u32(prev, 0);
-    FSAMP_TRACE(6);
-    if (prev != (unsigned)(p.S - 1)) return;
-    if (lane == 0)
-      __hip_atomic_store(&p.tickets[row * TICKET_STRIDE], 0u, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
-    if (p.stop == 5) {
-      if (lane == 0) p.out[row] = (int64_t)unpack_id(sm.top[0]);
-      return;
-    }
-    // 6. merge the S sorted lists of the row: stage them in LDS (every load in flight at
-    //    once), then fold them in registers
-    const int n = p.S * p.K;
-    const uint64_t* src = p.partials + (size_t)row * p.S * p.K;
-    for (int i = lane; i < n; i += 64)
-      sm.g.cand[i] = __hip_atomic_load(&src[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    FSAMP_TRACE(7);
-    if (p.K <= 64) wave_merge_lists<1>(sm.g.cand, p.S, p.K, sm.top);
-    else if (p.K <= 128) wave_merge_lists<2>(sm.g.cand, p.S, p.K, sm.top);
-    else if (p.K <= 256) wave_merge_lists<4>(sm.g.cand, p.S, p.K, sm.top);
-    else if (p.K <= 512) wave_merge_lists<8>(sm.g.cand, p.S, p.K, sm.top);
-    else wave_merge_lists<16>(sm.g.cand, p.S, p.K, sm.top);
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    FSAMP_TRACE(8);
-  }
-  if (p.stop == 5 || p.stop == 6) {
-    if (lane == 0) p.out[row] = (int64_t)unpack_id(sm.top[0]);
-    return;
-  }
-
-  // 7. sampling tail, or the candidate ids
-  if (p.ids != nullptr) {
-    for (int i = lane; i < p.K; i += 64) p.ids[(size_t)row * p.K + i] = (int64_t)unpack_id(sm.top[i]);
-    return;
-  }
-  run_tail(p, sm.top, p.K, row, u_row);
-  FSAMP_TRACE(9);
+  if (p.K <= 64) wave_back<1, NT>(p, sm, keff, ncand, sorted_in_lds, regions, row, split, u_row);
+  else if (p.K <= 128) wave_back<2, NT>(p, sm, keff, ncand, sorted_in_lds, regions, row, split, u_row);
+  else if (p.K <= 256) wave_back<4, NT>(p, sm, keff, ncand, sorted_in_lds, regions, row, split, u_row);
+  else if (p.K <= 512) wave_back<8, NT>(p, sm, keff, ncand, sorted_in_lds, regions, row, split, u_row);
+  else wave_back<16, NT>(p, sm, keff, ncand, sorted_in_lds, regions, row, split, u_row);
 }
 
 // ---- instantiation table -----------------------------------------------------------------------

@@ -41,7 +41,7 @@ def plan(B, V, k, splits=0, ptr=4096):
 
 
 @pytest.mark.parametrize("B,V,k,S,threads", [
-    (1, 151936, 50, 16, 256),     # C1: 16 splits of 9496 elements
+    (1, 151936, 50, 4, 512),      # C1: 4 splits of 37984 elements
     (64, 128256, 50, 2, 512),     # C2, B=64: 2 splits of 64128
     (16, 151936, 1024, 4, 1024),  # C4 k=1024: 4 splits, 4096 merged words
     (256, 151936, 50, 1, 512),    # C5: one workgroup per row, slice in VGPRs
