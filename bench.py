@@ -279,7 +279,7 @@ def main() -> int:
         f"{floor_graph_us:.2f}")
 
     traffic = None
-    tpath = os.path.join(ROOT, "profiles", "c5_hbm_traffic.json")
+    tpath = os.path.join(ROOT, "profiles", "fsamp_kernel_c5_hbm_traffic.json")
     if os.path.exists(tpath):
         with open(tpath) as f:
             traffic = json.load(f).get("bytes_per_launch")
