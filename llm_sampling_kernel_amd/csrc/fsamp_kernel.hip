@@ -139,7 +139,6 @@ struct Smem {
     uint32_t lb[1024];            // per-wave sorted thread maxima (lower bound)
   } u;
   int32_t wsum[2][16];         // per-wave partials for block scans (double-buffered)
-  int32_t wcnt[16];            // candidates gathered per wave
   int32_t misc[16];
 };
 
@@ -578,31 +577,22 @@ __device__ __forceinline__ void wave_back_wide(const Params& p, Smem<NT>& sm, in
                                                int split, float u_row);
 
 template <int RB, int NT>
+__device__ __forceinline__ void wave_tail_regs(const Params& p, Smem<NT>& sm, uint64_t (&v)[RB],
+                                               int keff, int row, int split, float u_row);
+
+template <int RB, int NT>
 __device__ __forceinline__ void wave_back(const Params& p, Smem<NT>& sm, int keff, int ncand, bool sorted_in_lds,
                           bool regions, int row, int split, float u_row) {
   if constexpr (RB > 4) {
     wave_back_wide<RB, NT>(p, sm, keff, ncand, sorted_in_lds, regions, row, split, u_row);
     return;
   }
-  constexpr int W = NT / 64;
-  constexpr int RW = FSAMP_K_MAX / W;
   const int l = lane_id();
   uint64_t v[RB];
   if (keff > 0 && !sorted_in_lds) {
-    // candidate e: per-wave regions are read through the prefix of the region counts
-    int cnt[W];
-#pragma unroll
-    for (int w = 0; w < W; ++w) cnt[w] = regions ? sm.wcnt[w] : 0;
+    // candidates are contiguous: in top[] from the gather, in cand[] from the radix select
     const uint64_t* base = regions ? sm.top : sm.g.cand;
-    auto load = [&](int e) -> uint64_t {
-      int a = e, pre = 0;
-#pragma unroll
-      for (int w = 1; w < W; ++w) {
-        pre += cnt[w - 1];
-        a += (regions && e >= pre) ? RW - cnt[w - 1] : 0;
-      }
-      return base[a];
-    };
+    auto load = [&](int e) -> uint64_t { return base[e]; };
     if (ncand <= 64 * RB) {
 #pragma unroll
       for (int i = 0; i < RB; ++i) {
@@ -631,6 +621,15 @@ __device__ __forceinline__ void wave_back(const Params& p, Smem<NT>& sm, int kef
 #pragma unroll
     for (int i = 0; i < RB; ++i) v[i] = 0ull;
   }
+  wave_tail_regs<RB, NT>(p, sm, v, keff, row, split, u_row);
+}
+
+// Wave 0 with the slice's sorted top keff in v[] (blocked by RB, zeros past keff): probe stop,
+// split hand-off and row merge when S > 1, then the ids or the sampling tail.
+template <int RB, int NT>
+__device__ __forceinline__ void wave_tail_regs(const Params& p, Smem<NT>& sm, uint64_t (&v)[RB],
+                                               int keff, int row, int split, float u_row) {
+  const int l = lane_id();
   FSAMP_TRACE(5);
   if (p.stop == 4) {
     if (l == 0 && split == 0) p.out[row] = keff > 0 ? (int64_t)unpack_id(v[0]) : -1;
@@ -693,23 +692,10 @@ template <int RB, int NT>
 __device__ __forceinline__ void wave_back_wide(const Params& p, Smem<NT>& sm, int keff, int ncand,
                                                bool sorted_in_lds, bool regions, int row,
                                                int split, float u_row) {
-  constexpr int W = NT / 64;
-  constexpr int RW = FSAMP_K_MAX / W;
   const int l = lane_id();
   if (keff > 0 && !sorted_in_lds) {
-    int cnt[W];
-#pragma unroll
-    for (int w = 0; w < W; ++w) cnt[w] = regions ? sm.wcnt[w] : 0;
     const uint64_t* base = regions ? sm.top : sm.g.cand;
-    auto load = [&](int e) -> uint64_t {
-      int a = e, pre = 0;
-#pragma unroll
-      for (int w = 1; w < W; ++w) {
-        pre += cnt[w - 1];
-        a += (regions && e >= pre) ? RW - cnt[w - 1] : 0;
-      }
-      return base[a];
-    };
+    auto load = [&](int e) -> uint64_t { return base[e]; };
     wave_sort_topk(load, ncand, keff, sm.top);
   }
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
@@ -763,14 +749,29 @@ __device__ __forceinline__ void wave_back_wide(const Params& p, Smem<NT>& sm, in
   FSAMP_RTRACE(1);
 }
 
+// lo + t*8 made opaque to the optimiser at each use site: element ids of chunk c are this plus
+// the constant c*NT*8, computed where they are needed, so that per-chunk ids are not hoisted
+// and kept live (one VGPR per chunk) across the phases that still hold the slice.
+__device__ __forceinline__ uint32_t opaque_base(int lo, int t) {
+  uint32_t b = (uint32_t)(lo + t * 8);
+  asm volatile("" : "+v"(b));
+  return b;
+}
+
+// compile-time integer for the pair ranges of the gather
+template <int N>
+struct IC {
+  static constexpr int value = N;
+};
+
 template <int NT, int CH, bool VEC>
 __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
-  constexpr int W = NT / 64;          // waves per workgroup
-  constexpr int NP = (CH + 1) / 2;    // chunk pairs
-  constexpr int RW = FSAMP_K_MAX / W; // per-wave candidate region in top[]
+  constexpr int W = NT / 64;                 // waves per workgroup
+  constexpr int NP = (CH + 1) / 2;           // chunk pairs
   __shared__ Smem<NT> sm;
   const int t = threadIdx.x;
-  const int lane = lane_id(), wid = t >> 6;
+  const int lane = lane_id();
+  const int wid = __builtin_amdgcn_readfirstlane(t >> 6);  // wave-uniform, known to the compiler
   const int row = blockIdx.x / p.S;
   const int split = blockIdx.x - row * p.S;
   const uint16_t* xr = p.logits + (size_t)row * (size_t)p.V;
@@ -789,41 +790,47 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
   //    load its last vector (a valid address) and are masked, so every load is unconditional
   //    and the key work on chunk c waits only for chunk c's load.
   uint32_t kv[CH][4];
-  if (count > 0) {
+  auto load_slice = [&]() {
+    if (count > 0) {
 #pragma unroll
-    for (int c = 0; c < CH; ++c) {
-      const int e0 = lo + (c * NT + t) * 8;
-      if constexpr (VEC) {
-        const uint4 v = *reinterpret_cast<const uint4*>(xr + min(e0, hi - 8));
-        kv[c][0] = v.x;
-        kv[c][1] = v.y;
-        kv[c][2] = v.z;
-        kv[c][3] = v.w;
-      } else {
+      for (int c = 0; c < CH; ++c) {
+        const int e0 = lo + (c * NT + t) * 8;
+        if constexpr (VEC) {
+          const uint4 v = *reinterpret_cast<const uint4*>(xr + min(e0, hi - 8));
+          kv[c][0] = v.x;
+          kv[c][1] = v.y;
+          kv[c][2] = v.z;
+          kv[c][3] = v.w;
+        } else {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int e = e0 + 2 * q;
-          const uint32_t a = (e < hi) ? (uint32_t)xr[e] : 0u;
-          const uint32_t b = (e + 1 < hi) ? (uint32_t)xr[e + 1] : 0u;
-          kv[c][q] = a | (b << 16);
+          for (int q = 0; q < 4; ++q) {
+            const int e = e0 + 2 * q;
+            const uint32_t a = (e < hi) ? (uint32_t)xr[e] : 0u;
+            const uint32_t b = (e + 1 < hi) ? (uint32_t)xr[e + 1] : 0u;
+            kv[c][q] = a | (b << 16);
+          }
         }
       }
-    }
-  } else {
+    } else {
 #pragma unroll
-    for (int c = 0; c < CH; ++c) kv[c][0] = kv[c][1] = kv[c][2] = kv[c][3] = 0u;
-  }
+      for (int c = 0; c < CH; ++c) kv[c][0] = kv[c][1] = kv[c][2] = kv[c][3] = 0u;
+    }
+  };
+  load_slice();
   // pm[i]: packed 16-bit maxima over the two chunks of pair i (even halves, odd halves); a
   // pair holds an element >= X iff pkmax(pm[i], (X-1) in both halves) differs from the latter
   uint32_t pm[NP];
-#pragma unroll
-  for (int c = 0; c < CH; ++c) {
+  // vector chunks of this thread inside the slice are those with c*NT < nv_left (one register
+  // and a compare with a constant per chunk, instead of a per-chunk address kept live)
+  const int nv_left = (count >> 3) - t;
+  auto convert = [&](int c) {
     const int e0 = lo + (c * NT + t) * 8;
+    const bool in_slice = c * NT < nv_left;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       uint32_t k = keys2(kv[c][q]);
       if constexpr (VEC) {
-        if (e0 >= hi) k = 0u;
+        if (!in_slice) k = 0u;
       } else {
         const int e = e0 + 2 * q;
         if (e >= hi) k &= 0xFFFF0000u;
@@ -833,17 +840,148 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
     }
     const uint32_t m2 = pkmax(pkmax(kv[c][0], kv[c][1]), pkmax(kv[c][2], kv[c][3]));
     pm[c >> 1] = (c & 1) ? pkmax(pm[c >> 1], m2) : m2;
-  }
-  uint32_t tm2 = pm[0];
+  };
+  auto tmax_of = [&](auto i0c, auto i1c) -> uint32_t {
+    constexpr int I0 = decltype(i0c)::value, I1 = decltype(i1c)::value;
+    uint32_t m = 0;
 #pragma unroll
-  for (int i = 1; i < NP; ++i) tm2 = pkmax(tm2, pm[i]);
-  const uint32_t tmax = max(tm2 & 0xFFFFu, tm2 >> 16);
-  FSAMP_TRACE(1);
+    for (int i = I0; i < I1; ++i) m = pkmax(m, pm[i]);
+    return max(m & 0xFFFFu, m >> 16);
+  };
   // pair of chunk c holds an element >= X (X >= 1)
   auto pair_ge = [&](int c, uint32_t X) -> bool {
     const uint32_t xm1 = (X - 1u) * 0x10001u;
     return pkmax(pm[c >> 1], xm1) != xm1;
   };
+
+  // 2. lower bound L of the keff-th largest key among the given thread maxima (keff <= NT by
+  //    plan): the keff-th largest of the union of every wave's top-m thread maxima,
+  //    m = max(ceil(keff/W), 64/W).  Maxima are made unique by the thread index in the low
+  //    bits.  Each wave sorts its 64 maxima with the DPP network and publishes the top m;
+  //    after one barrier every wave sorts the W*m published words itself (no second barrier).
+  //    Past 256 published words (keff > 256, where the candidates go through the radix select
+  //    anyway) the looser bound min over waves of the wave's m-th maximum is used instead:
+  //    every wave then has m threads, W*m >= keff in all, whose maximum is >= L.  It keeps the
+  //    register sort of more than 256 words out of the phase that still holds the slice.
+  auto lower_bound = [&](uint32_t tm) -> uint32_t {
+    const int m = min(64, max((keff + W - 1) / W, 64 / W));
+    const int n = W * m;
+    const uint32_t srt = wave_sort_desc<uint32_t>((tm << 10) | (uint32_t)t);
+    if (n <= WSORT_MAX) {
+      if (lane < m) sm.u.lb[wid * m + lane] = srt;
+    } else {
+      if (lane == m - 1) sm.u.lb[wid] = srt;
+    }
+    __syncthreads();
+    FSAMP_TRACE(2);
+    uint32_t kth;
+    if (n <= 64) {
+      kth = wave_kth_u32<1>(sm.u.lb, n, keff);
+    } else if (n <= 128) {
+      kth = wave_kth_u32<2>(sm.u.lb, n, keff);
+    } else if (n <= WSORT_MAX) {
+      kth = wave_kth_u32<4>(sm.u.lb, n, keff);
+    } else {
+      kth = lane < W ? sm.u.lb[lane] : 0xFFFFFFFFu;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) kth = min(kth, (uint32_t)__shfl_xor((int)kth, d, 64));
+    }
+    FSAMP_TRACE(3);
+    return max(kth >> 10, 1u);
+  };
+
+  // 3. gather the elements >= L of pairs [I0, I1) into region_base[0, rw): each wave takes
+  //    its slots with one LDS atomic on the counter *wc (slots past rw are counted, not
+  //    written; more than WSORT_MAX sends the slice to the radix path).  Only threads with a
+  //    pair >= L hold any, typically one pair each, so one pass over the pair maxima stages up
+  //    to STAGE_SLOTS qualifying pairs per thread in LDS (two compares per pair, the pair
+  //    stored under an exec mask), and the candidates are then extracted from the staged
+  //    copies, where a runtime element index is an address instead of a select chain over the
+  //    register array.  A thread with more qualifying pairs than slots gathers from its
+  //    registers instead (per-chunk branches).
+  auto stage = [&](auto i0c, auto i1c, uint32_t L, int& nst) {
+    constexpr int I0 = decltype(i0c)::value, I1 = decltype(i1c)::value;
+    const uint32_t lm1 = (L - 1u) * 0x10001u;
+#pragma unroll
+    for (int i = I0; i < I1; ++i) {
+      const bool hit = pkmax(pm[i], lm1) != lm1;
+      if (hit && nst < STAGE_SLOTS) {
+        sm.g.st.a[nst][t] = make_uint4(kv[2 * i][0], kv[2 * i][1], kv[2 * i][2], kv[2 * i][3]);
+        if (2 * i + 1 < CH)
+          sm.g.st.b[nst][t] = make_uint4(kv[2 * i + 1][0], kv[2 * i + 1][1], kv[2 * i + 1][2],
+                                         kv[2 * i + 1][3]);
+        else
+          sm.g.st.b[nst][t] = make_uint4(0u, 0u, 0u, 0u);
+        sm.meta[nst][t] = (uint8_t)i;
+      }
+      nst += hit ? 1 : 0;
+    }
+  };
+  auto extract = [&](uint32_t L, int nst, uint64_t* region_base, int rw, int32_t* wc) {
+    constexpr int C0 = 0, C1 = CH;
+    FSAMP_TRACE(13);
+    const bool from_regs = nst > STAGE_SLOTS;
+    auto staged_mask = [&](int s) -> uint32_t {
+      const uint4 a = sm.g.st.a[s][t], b = sm.g.st.b[s][t];
+      const uint32_t ka[4] = {a.x, a.y, a.z, a.w}, kb[4] = {b.x, b.y, b.z, b.w};
+      return ge_mask(ka, L) | (ge_mask(kb, L) << 8);
+    };
+    int mine = 0;
+    if (from_regs) {
+#pragma unroll
+      for (int c = C0; c < C1; ++c)
+        if (pair_ge(c, L)) mine += __popc(ge_mask(kv[c], L));
+    } else {
+      for (int s = 0; s < nst; ++s) mine += __popc(staged_mask(s));
+    }
+    FSAMP_TRACE(10);
+    if (__ballot(mine > 0) != 0ull) {
+      const uint32_t incl = wave_incl_scan_u32((uint32_t)mine);
+      int base = 0;
+      if (lane == 63) base = atomicAdd(wc, (int)incl);
+      int slot = __builtin_amdgcn_readlane(base, 63) + (int)incl - mine;
+      uint64_t* region = region_base;
+      FSAMP_TRACE(11);
+      if (from_regs) {
+        const uint32_t idb = opaque_base(lo, t);
+#pragma unroll
+        for (int c = C0; c < C1; ++c) {
+          if (pair_ge(c, L)) {
+            uint32_t m = ge_mask(kv[c], L);
+            const uint32_t id0 = idb + (uint32_t)(c * NT * 8);
+            while (m != 0u) {
+              const int j = __ffs(m) - 1;
+              m &= m - 1u;
+              if (slot < rw) region[slot] = pack(key_at(kv[c], j), id0 + (uint32_t)j);
+              ++slot;
+            }
+          }
+        }
+      } else {
+        const uint32_t idb = opaque_base(lo, t);
+        for (int s = 0; s < nst; ++s) {
+          uint32_t m = staged_mask(s);
+          const int c0 = 2 * (int)sm.meta[s][t];
+          const uint16_t* ka = reinterpret_cast<const uint16_t*>(&sm.g.st.a[s][t]);
+          const uint16_t* kb = reinterpret_cast<const uint16_t*>(&sm.g.st.b[s][t]);
+          while (m != 0u) {
+            const int j = __ffs(m) - 1;
+            m &= m - 1u;
+            const uint32_t key = j < 8 ? ka[j] : kb[j - 8];
+            const uint32_t id = idb + (uint32_t)(((c0 + (j >> 3)) * NT) * 8 + (j & 7));
+            if (slot < rw) region[slot] = pack(key, id);
+            ++slot;
+          }
+        }
+      }
+    }
+    FSAMP_TRACE(12);
+  };
+
+#pragma unroll
+  for (int c = 0; c < CH; ++c) convert(c);
+  FSAMP_TRACE(1);
+  const uint32_t tmax = tmax_of(IC<0>{}, IC<NP>{});
 
   if (p.stop == 1) {
     const uint32_t wmax = wave_max_u32(tmax);
@@ -855,142 +993,25 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
     return;
   }
 
+  // Single-phase selection: L from every thread maximum, one gather, and the exact radix
+  // select when the candidates overflow.
   int ncand = 0;
   bool sorted_in_lds = false;
   bool regions = true;  // candidates in per-wave regions of top[] (else contiguous in cand[])
   if (keff > 0) {
-    // 2. lower bound L of the slice's keff-th largest key (keff <= NT by plan): the
-    //    keff-th largest of the union of every wave's top-m thread maxima, m = ceil(keff/W).
-    //    Maxima are made unique by the thread index in the low bits.  Each wave sorts its 64
-    //    maxima with the DPP network and publishes the top m; after one barrier every wave
-    //    sorts the W*m published words itself (no second barrier).  Past 256 published words
-    //    (keff > 256, where the candidates go through the radix select anyway) the looser
-    //    bound min over waves of the wave's m-th maximum is used instead: every wave then has
-    //    m threads, W*m >= keff in all, whose maximum is >= L.  It keeps the register sort of
-    //    more than 256 words out of the phase that still holds the slice in registers.
-    uint32_t L;
-    {
-      const int m = min(64, (keff + W - 1) / W);
-      const int n = W * m;
-      const uint32_t srt = wave_sort_desc<uint32_t>((tmax << 10) | (uint32_t)t);
-      if (n <= WSORT_MAX) {
-        if (lane < m) sm.u.lb[wid * m + lane] = srt;
-      } else {
-        if (lane == m - 1) sm.u.lb[wid] = srt;
-      }
-      __syncthreads();
-      FSAMP_TRACE(2);
-      uint32_t kth;
-      if (n <= 64) {
-        kth = wave_kth_u32<1>(sm.u.lb, n, keff);
-      } else if (n <= 128) {
-        kth = wave_kth_u32<2>(sm.u.lb, n, keff);
-      } else if (n <= WSORT_MAX) {
-        kth = wave_kth_u32<4>(sm.u.lb, n, keff);
-      } else {
-        kth = lane < W ? sm.u.lb[lane] : 0xFFFFFFFFu;
-#pragma unroll
-        for (int d = 1; d < 64; d <<= 1) kth = min(kth, (uint32_t)__shfl_xor((int)kth, d, 64));
-      }
-      L = max(kth >> 10, 1u);
-      FSAMP_TRACE(3);
-    }
+    const uint32_t L = lower_bound(tmax);
     if (p.stop == 2) {
       if (t == 0 && split == 0) p.out[row] = (int64_t)L;
       return;
     }
-
-    // 3. gather the elements >= L into top[], wave w into top[w*RW, (w+1)*RW) (slots past a
-    //    region are counted, not written; an overfull region sends the slice to the radix path).  Only threads with a pair >= L hold any, typically one pair each, so one
-    //    pass over the pair maxima stages up to STAGE_SLOTS qualifying pairs per thread in LDS
-    //    (two compares per pair, the pair stored under an exec mask), and the candidates are
-    //    then extracted from the staged copies, where a runtime element index is an address
-    //    instead of a select chain over the register array.  A thread with more qualifying
-    //    pairs than slots gathers from its registers instead (per-chunk branches).
-    {
-      const uint32_t lm1 = (L - 1u) * 0x10001u;
-      int nst = 0;
-#pragma unroll
-      for (int i = 0; i < NP; ++i) {
-        const bool hit = pkmax(pm[i], lm1) != lm1;
-        if (hit && nst < STAGE_SLOTS) {
-          sm.g.st.a[nst][t] = make_uint4(kv[2 * i][0], kv[2 * i][1], kv[2 * i][2], kv[2 * i][3]);
-          if (2 * i + 1 < CH)
-            sm.g.st.b[nst][t] = make_uint4(kv[2 * i + 1][0], kv[2 * i + 1][1], kv[2 * i + 1][2],
-                                           kv[2 * i + 1][3]);
-          else
-            sm.g.st.b[nst][t] = make_uint4(0u, 0u, 0u, 0u);
-          sm.meta[nst][t] = (uint8_t)i;
-        }
-        nst += hit ? 1 : 0;
-      }
-      FSAMP_TRACE(13);
-      const bool from_regs = nst > STAGE_SLOTS;
-      auto staged_mask = [&](int s) -> uint32_t {
-        const uint4 a = sm.g.st.a[s][t], b = sm.g.st.b[s][t];
-        const uint32_t ka[4] = {a.x, a.y, a.z, a.w}, kb[4] = {b.x, b.y, b.z, b.w};
-        return ge_mask(ka, L) | (ge_mask(kb, L) << 8);
-      };
-      int mine = 0;
-      if (from_regs) {
-#pragma unroll
-        for (int c = 0; c < CH; ++c)
-          if (pair_ge(c, L)) mine += __popc(ge_mask(kv[c], L));
-      } else {
-        for (int s = 0; s < nst; ++s) mine += __popc(staged_mask(s));
-      }
-      FSAMP_TRACE(10);
-      uint32_t wtot = 0;
-      if (__ballot(mine > 0) != 0ull) {
-        const uint32_t incl = wave_incl_scan_u32((uint32_t)mine);
-        wtot = read_lane_u32(incl, 63);
-        int slot = (int)incl - mine;
-        uint64_t* region = sm.top + wid * RW;
-        FSAMP_TRACE(11);
-        if (from_regs) {
-#pragma unroll
-          for (int c = 0; c < CH; ++c) {
-            if (pair_ge(c, L)) {
-              uint32_t m = ge_mask(kv[c], L);
-              const uint32_t id0 = (uint32_t)(lo + (c * NT + t) * 8);
-              while (m != 0u) {
-                const int j = __ffs(m) - 1;
-                m &= m - 1u;
-                if (slot < RW) region[slot] = pack(key_at(kv[c], j), id0 + (uint32_t)j);
-                ++slot;
-              }
-            }
-          }
-        } else {
-          for (int s = 0; s < nst; ++s) {
-            uint32_t m = staged_mask(s);
-            const int c0 = 2 * (int)sm.meta[s][t];
-            const uint16_t* ka = reinterpret_cast<const uint16_t*>(&sm.g.st.a[s][t]);
-            const uint16_t* kb = reinterpret_cast<const uint16_t*>(&sm.g.st.b[s][t]);
-            while (m != 0u) {
-              const int j = __ffs(m) - 1;
-              m &= m - 1u;
-              const uint32_t key = j < 8 ? ka[j] : kb[j - 8];
-              const uint32_t id = (uint32_t)(lo + ((c0 + (j >> 3)) * NT + t) * 8 + (j & 7));
-              if (slot < RW) region[slot] = pack(key, id);
-              ++slot;
-            }
-          }
-        }
-      }
-      if (lane == 0) sm.wcnt[wid] = (int)wtot;
-      FSAMP_TRACE(12);
-    }
+    int nst = 0;
+    stage(IC<0>{}, IC<NP>{}, L, nst);
+    extract(L, nst, sm.top, FSAMP_K_MAX, &sm.misc[M_CNT]);
     __syncthreads();
     FSAMP_TRACE(4);
-    int total = 0;
-    bool wave_over = false;
-#pragma unroll
-    for (int w = 0; w < W; ++w) {
-      const int n = sm.wcnt[w];
-      total += n;
-      wave_over |= n > RW;
-    }
+    // LDS loads count as divergent to the compiler; the total is uniform by construction
+    const int total = __builtin_amdgcn_readfirstlane(sm.misc[M_CNT]);
+    const bool wave_over = false;
     if (p.stop == 3) {
       if (t == 0 && split == 0) p.out[row] = total;
       return;
@@ -1059,7 +1080,7 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
       for (int c = 0; c < CH; ++c) {
         if (pair_ge(c, T + 1u)) {
           uint32_t m = ge_mask(kv[c], T + 1u);
-          const uint32_t id0 = (uint32_t)(lo + (c * NT + t) * 8);
+          const uint32_t id0 = opaque_base(lo, t) + (uint32_t)(c * NT * 8);
           while (m != 0u) {
             const int j = __ffs(m) - 1;
             m &= m - 1u;
@@ -1079,7 +1100,7 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
           uint32_t tiemask = eq_mask(kv[c], T);
           int chunk_total = 0;
           int rank = taken + block_excl_scan<NT>(__popc(tiemask), &chunk_total, sm.wsum[c & 1]);
-          const uint32_t id0 = (uint32_t)(lo + (c * NT + t) * 8);
+          const uint32_t id0 = opaque_base(lo, t) + (uint32_t)(c * NT * 8);
           while (tiemask != 0u && rank < need) {
             const int j = __ffs(tiemask) - 1;
             tiemask &= tiemask - 1u;

@@ -2,12 +2,12 @@
 // ds_bpermute, shared by the sampler kernel and its lane-layout tests.
 //
 // DPP moves (__builtin_amdgcn_update_dpp) are VALU operations with a few cycles of latency;
-// ds_bpermute (what __shfl_* compiles to) round-trips through the LDS crossbar.  The sorting
-// networks and scans here sit on the critical path of a call, so each lane distance uses the
-// cheapest form the hardware has:
+// ds_swizzle and ds_bpermute (what __shfl_* compiles to) round-trip through the LDS crossbar.
+// The sorting networks and scans here sit on the critical path of a call, so each lane
+// distance uses the cheapest form gfx950 has, all of them VALU:
 //   xor 1, 2   quad_perm                      xor 8   row_ror:8 (a 16-lane row rotated by 8)
-//   xor 4      row_shl:4 / row_shr:4 + select xor 16  ds_swizzle (bit mode, xor_mask 16)
-//   xor 32     ds_bpermute
+//   xor 4      row_shl:4 / row_shr:4 + select xor 16  v_permlane16_swap + select
+//   xor 32     v_permlane32_swap + select
 // and the inclusive scan uses row_shr:1,2,4,8 inside 16-lane rows, then row_bcast:15 and
 // row_bcast:31 across rows.
 #pragma once
@@ -47,10 +47,15 @@ __device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
   } else if constexpr (J == 8) {
     return (uint32_t)__builtin_amdgcn_update_dpp(0, x, DPP_ROW_ROR8, 0xF, 0xF, false);
   } else if constexpr (J == 16) {
-    return (uint32_t)__builtin_amdgcn_ds_swizzle(x, (16 << 10) | 0x1F);
+    // swap(v, v): result[0] (vdst) has the even 16-lane rows' values in the odd rows,
+    // result[1] (vsrc) the odd rows' values in the even rows
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return (lane_id() & 16) ? r[0] : r[1];
   } else {
     static_assert(J == 32, "lane distance");
-    return (uint32_t)__shfl_xor(x, 32, 64);
+    // the same with the two 32-lane halves
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return (lane_id() & 32) ? r[0] : r[1];
   }
 }
 
@@ -147,14 +152,14 @@ __device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v) {
 // (lane 0, i = 0) with the largest word.  Distances J < R stay inside a lane; larger ones pair
 // lane l with lane l ^ (J / R).
 
-template <int R, int K, int J>
+template <int R, int K, int J, bool ASC = false>
 __device__ __forceinline__ void net_stage(uint64_t (&v)[R]) {
   const int l = lane_id();
   if constexpr (J < R) {
 #pragma unroll
     for (int i = 0; i < R; ++i) {
       if ((i & J) == 0) {
-        const bool desc = (((l * R + i) & K) == 0);
+        const bool desc = (((l * R + i) & K) == 0) != ASC;
         const uint64_t a = v[i], b = v[i + J];
         if ((a < b) == desc) {
           v[i] = b;
@@ -167,7 +172,7 @@ __device__ __forceinline__ void net_stage(uint64_t (&v)[R]) {
     for (int i = 0; i < R; ++i) {
       const uint64_t o = xor_lane64<J / R>(v[i]);
       const int e = l * R + i;
-      const bool desc = (e & K) == 0;
+      const bool desc = ((e & K) == 0) != ASC;
       const bool lower = (e & J) == 0;
       const uint64_t hi = v[i] > o ? v[i] : o, lo = v[i] > o ? o : v[i];
       v[i] = (lower == desc) ? hi : lo;
@@ -175,16 +180,16 @@ __device__ __forceinline__ void net_stage(uint64_t (&v)[R]) {
   }
 }
 
-template <int R, int K, int J>
+template <int R, int K, int J, bool ASC = false>
 __device__ __forceinline__ void net_merge(uint64_t (&v)[R]) {
-  net_stage<R, K, J>(v);
-  if constexpr (J > 1) net_merge<R, K, J / 2>(v);
+  net_stage<R, K, J, ASC>(v);
+  if constexpr (J > 1) net_merge<R, K, J / 2, ASC>(v);
 }
 
-template <int R, int K>
+template <int R, int K, bool ASC = false>
 __device__ __forceinline__ void net_sort_levels(uint64_t (&v)[R]) {
-  if constexpr (K > 2) net_sort_levels<R, K / 2>(v);
-  net_merge<R, K, K / 2>(v);
+  if constexpr (K > 2) net_sort_levels<R, K / 2, ASC>(v);
+  net_merge<R, K, K / 2, ASC>(v);
 }
 
 // Full descending sort of the 64*R words.
