@@ -18,12 +18,13 @@
  * Workspace.  Rows are split over `splits` workgroups and the last workgroup of a row to
  * finish merges the row (one launch per call).  That needs `fsamp_workspace_bytes(...)`
  * bytes of device workspace laid out as [per-row counters: round_up(128*B, 256) bytes]
- * [per-split candidates].  The counter region must be zero before a call
- * (fsamp_workspace_init zeroes the whole buffer on the stream) and every call leaves it zero
- * again; the candidate region is scratch.  A buffer reused with a larger B must be zeroed
- * again, because the larger counter region overlaps the old candidates.  Calls that share
- * one workspace must not run concurrently.  A plan with splits == 1 needs no workspace
- * (size 0, ws may be NULL).
+ * [one grid counter: 256 bytes][per-split candidates].  The counter regions must be zero
+ * before a call (fsamp_workspace_init zeroes the whole buffer on the stream) and every call
+ * leaves them zero again; the candidate region is scratch.  A buffer reused with a larger B
+ * must be zeroed again, because the larger counter region overlaps the old candidates.
+ * Calls that share one workspace must not run concurrently.  A call whose plan has
+ * splits == 1 and that uses no offset counter (fsamp_sample_ex) reads no workspace: ws may
+ * then be NULL.
  */
 #ifndef FSAMP_H
 #define FSAMP_H
@@ -95,6 +96,41 @@ int fsamp_workspace_init(void* ws, size_t bytes, hipStream_t stream);
 int fsamp_sample(const void* logits, int dtype, int64_t B, int64_t V, int64_t top_k,
                  double top_p, const float* u, uint64_t seed, uint64_t offset, int64_t* out,
                  void* ws, size_t ws_bytes, int64_t splits_override, hipStream_t stream);
+
+/*
+ * Per-row sampling controls and the graph-safe draw of fsamp_sample_ex.  Every pointer may be
+ * NULL (the call's scalar value applies).  Device arrays of B entries:
+ *   top_k[b]        row b samples from its top min(max(top_k[b], 1), k) ranks: a prefix of
+ *                   the call's top-k selection (int32);
+ *   top_p[b]        row b's nucleus threshold (fp32): ranks are kept while the exclusive
+ *                   prefix is < top_p[b]; >= 1 keeps all, <= 0 keeps rank 0 only;
+ *   temperature[b]  row b's softmax runs on (x - max) * (1 / temperature[b]) in fp32;
+ *                   temperature[b] <= 0 (or NaN) is greedy: rank 0.
+ * offset_counter    device uint64: when u == NULL, the row uniforms are
+ *                   splitmix64(seed, *offset_counter, row) and the call adds 4 to the counter
+ *                   once every row has drawn (in the kernel, so a captured HIP graph advances
+ *                   it on every replay).  The call's `offset` argument is then ignored.  The
+ *                   grid counter in the workspace is used, so ws is required.
+ * No counterpart in the reference for the per-row arrays (SEMANTICS.md lists them as open);
+ * the counter replaces the graph-capturable generator path of sample_fused with offset < 0
+ * (csrc/fused_sampling.cu:112-118, :441-447).
+ */
+typedef struct fsamp_row_params {
+  const int32_t* top_k;
+  const float* top_p;
+  const float* temperature;
+  uint64_t* offset_counter;
+} fsamp_row_params;
+
+/*
+ * fsamp_stages with per-row controls (rows may be NULL: then it is fsamp_stages, or
+ * fsamp_sample when keep and renormed are NULL too).  keep / renormed are [B, k] with ranks at
+ * or past a row's own k written as 0.
+ */
+int fsamp_sample_ex(const void* logits, int dtype, int64_t B, int64_t V, int64_t top_k,
+                    double top_p, const float* u, uint64_t seed, uint64_t offset,
+                    const fsamp_row_params* rows, int64_t* out, uint8_t* keep, float* renormed,
+                    void* ws, size_t ws_bytes, int64_t splits_override, hipStream_t stream);
 
 /*
  * Debug form of fsamp_sample that also writes, per row and rank i < k,

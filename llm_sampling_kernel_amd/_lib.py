@@ -27,6 +27,11 @@ class Plan(ctypes.Structure):
                 ("reserved", _i32), ("workspace_bytes", _sz)]
 
 
+class RowParams(ctypes.Structure):
+    """fsamp_row_params: per-row controls and the graph-safe offset counter (device pointers)."""
+    _fields_ = [("top_k", _vp), ("top_p", _vp), ("temperature", _vp), ("offset_counter", _vp)]
+
+
 class AttrRow(ctypes.Structure):
     _fields_ = [("name", ctypes.c_char * 64), ("threads", _i32), ("chunks", _i32),
                 ("vgprs", _i32), ("scratch_bytes", _i32), ("lds_bytes", _i32),
@@ -42,6 +47,8 @@ SIGNATURES = {
                             _i64, _vp]),
     "fsamp_stages": (_i32, [_vp, _i32, _i64, _i64, _i64, _dbl, _vp, _u64, _u64, _vp, _vp, _vp,
                             _vp, _sz, _i64, _vp]),
+    "fsamp_sample_ex": (_i32, [_vp, _i32, _i64, _i64, _i64, _dbl, _vp, _u64, _u64,
+                               ctypes.POINTER(RowParams), _vp, _vp, _vp, _vp, _sz, _i64, _vp]),
     "fsamp_topk": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _sz, _i64, _vp]),
     "fsamp_probe_phase": (_i32, [_vp, _i32, _i64, _i64, _i64, _dbl, _i64, _vp, _vp, _sz, _i64,
                                  _vp]),

@@ -21,6 +21,7 @@ size_t round_up(size_t a, size_t b) { return (a + b - 1) / b * b; }
 
 // per-row arrival counters, one 128-byte line each (atomics on one line serialise)
 size_t counter_bytes(int64_t B) { return round_up((size_t)B * TICKET_STRIDE * 4u, 256); }
+constexpr size_t kGridCounterBytes = 256;  // the grid counter of the graph-safe draw
 
 // Tiling preference forced by fsamp_debug_force_threads (0 = automatic).
 int g_force_threads = 0;
@@ -100,8 +101,8 @@ int make_plan_impl(const void* logits, int64_t B, int64_t V, int64_t top_k, int6
   pl->chunks = e->chunks;
   pl->vec = vec ? 1 : 0;
   pl->reserved = 0;
-  pl->workspace_bytes =
-      S > 1 ? counter_bytes(B) + (size_t)B * (size_t)S * (size_t)K * 8u : 0u;
+  pl->workspace_bytes = counter_bytes(B) + kGridCounterBytes +
+                        (S > 1 ? (size_t)B * (size_t)S * (size_t)K * 8u : 0u);
   if (kern) *kern = e;
   return FSAMP_OK;
 }
@@ -115,7 +116,8 @@ __global__ void fill_zero_kernel(uint32_t* p, size_t n) {
 int launch(const void* logits, int dtype, int64_t B, int64_t V, int64_t top_k, double top_p,
            const float* u, uint64_t seed, uint64_t offset, int64_t* out, int64_t* ids,
            uint8_t* keep, float* renormed, int stop, void* ws, size_t ws_bytes,
-           int64_t splits_override, hipStream_t stream, int64_t* trace = nullptr) {
+           int64_t splits_override, hipStream_t stream, int64_t* trace = nullptr,
+           const fsamp_row_params* rows = nullptr) {
   int rc = validate(dtype, B, V, top_k);
   if (rc != FSAMP_OK) return rc;
   if (!(top_p > 0.0 && top_p <= 1.0)) return FSAMP_ERR_TOPP;
@@ -125,7 +127,8 @@ int launch(const void* logits, int dtype, int64_t B, int64_t V, int64_t top_k, d
   const KernelEntry* e = nullptr;
   rc = make_plan_impl(logits, B, V, top_k, splits_override, &pl, &e);
   if (rc != FSAMP_OK) return rc;
-  if (pl.workspace_bytes > 0 && (ws == nullptr || ws_bytes < pl.workspace_bytes))
+  const bool use_ctr = rows != nullptr && rows->offset_counter != nullptr && u == nullptr;
+  if ((pl.splits > 1 || use_ctr) && (ws == nullptr || ws_bytes < pl.workspace_bytes))
     return FSAMP_ERR_WORKSPACE;
   Params p;
   p.logits = static_cast<const uint16_t*>(logits);
@@ -137,9 +140,16 @@ int launch(const void* logits, int dtype, int64_t B, int64_t V, int64_t top_k, d
   p.seed = seed;
   p.offset = offset;
   p.tickets = static_cast<uint32_t*>(ws);
-  p.partials = pl.workspace_bytes > 0
-                   ? reinterpret_cast<uint64_t*>(static_cast<char*>(ws) + counter_bytes(B))
-                   : nullptr;
+  p.grid_ticket = ws != nullptr
+                      ? reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + counter_bytes(B))
+                      : nullptr;
+  p.partials = pl.splits > 1 ? reinterpret_cast<uint64_t*>(static_cast<char*>(ws) +
+                                                           counter_bytes(B) + kGridCounterBytes)
+                             : nullptr;
+  p.offset_ctr = use_ctr ? reinterpret_cast<uint64_t*>(rows->offset_counter) : nullptr;
+  p.topk_row = rows != nullptr ? rows->top_k : nullptr;
+  p.topp_row = rows != nullptr ? rows->top_p : nullptr;
+  p.temp_row = rows != nullptr ? rows->temperature : nullptr;
   p.B = (int)B;
   p.V = (int)V;
   p.K = (int)pl.k;
@@ -216,6 +226,15 @@ int fsamp_sample(const void* logits, int dtype, int64_t B, int64_t V, int64_t to
   if (out == nullptr) return FSAMP_ERR_NULL;
   return launch(logits, dtype, B, V, top_k, top_p, u, seed, offset, out, nullptr, nullptr,
                 nullptr, 7, ws, ws_bytes, splits_override, stream);
+}
+
+int fsamp_sample_ex(const void* logits, int dtype, int64_t B, int64_t V, int64_t top_k,
+                    double top_p, const float* u, uint64_t seed, uint64_t offset,
+                    const fsamp_row_params* rows, int64_t* out, uint8_t* keep, float* renormed,
+                    void* ws, size_t ws_bytes, int64_t splits_override, hipStream_t stream) {
+  if (out == nullptr) return FSAMP_ERR_NULL;
+  return launch(logits, dtype, B, V, top_k, top_p, u, seed, offset, out, nullptr, keep, renormed,
+                7, ws, ws_bytes, splits_override, stream, nullptr, rows);
 }
 
 int fsamp_stages(const void* logits, int dtype, int64_t B, int64_t V, int64_t top_k,

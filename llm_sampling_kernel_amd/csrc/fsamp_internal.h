@@ -23,6 +23,11 @@ struct Params {
   uint64_t seed, offset;
   uint64_t* partials;      // workspace: [B, S, K] per-split candidates
   uint32_t* tickets;       // workspace: [B] arrival counters, zero between calls
+  uint32_t* grid_ticket;   // workspace: rows that have drawn from *offset_ctr, zero between calls
+  uint64_t* offset_ctr;    // graph-safe draw offset (device) or nullptr
+  const int32_t* topk_row; // per-row k, top_p, temperature (device) or nullptr
+  const float* topp_row;
+  const float* temp_row;
   int B, V, K, S;
   int slice;               // elements per split, a multiple of 8
   float top_p_f;           // (float)top_p

@@ -383,9 +383,32 @@ __device__ __forceinline__ void wave_merge_lists(const uint64_t* lists, int S, i
 // the words stay in LDS).  Per-lane sums are serial, lane values are combined by
 // wave_incl_scan_f32's fixed association (z = its last lane; the prefix offset of lane l = its
 // value at lane l-1).  The CPU oracle evaluates the same operations in the same order.
+// A row's sampling controls, read at kernel start so that their latency hides under the loads.
+struct RowCtl {
+  float u;       // the row's uniform
+  int k;         // ranks the row samples from (<= K): a prefix of the top-K selection
+  float top_p;   // nucleus threshold
+  int keep_all;  // top_p >= 1
+  float inv_t;   // 1 / temperature (exactly 1 when the call has none)
+};
+
+// Graph-safe draw: once every row has taken its uniform from *offset_ctr, the last one adds 4
+// to it for the next call (lane 0 of the row's finishing wave).
+__device__ __forceinline__ void advance_offset(const Params& p) {
+  if (p.offset_ctr == nullptr || lane_id() != 0) return;
+  const unsigned n = __hip_atomic_fetch_add(p.grid_ticket, 1u, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+  if (n == (unsigned)(p.B - 1)) {
+    __hip_atomic_store(p.grid_ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_fetch_add(p.offset_ctr, (uint64_t)4, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
 template <int RB, bool FROM_LDS>
 __device__ __forceinline__ void sample_tail(const Params& p, const uint64_t (&v)[RB],
-                                            const uint64_t* top, int K, int row, float u) {
+                                            const uint64_t* top, const RowCtl& rc, int row) {
+  const int K = rc.k;
+  const float u = rc.u;
   const int l = lane_id();
   const int R = (K + 63) >> 6;
   const int base = l * R;
@@ -402,7 +425,7 @@ __device__ __forceinline__ void sample_tail(const Params& p, const uint64_t (&v)
     w[j] = 0.0f;
     if (j < R && base + j < K) {
       const float x = key_to_float((uint32_t)(word(j) >> 32), p.is_bf16);
-      w[j] = exp_nonpos(x - m);
+      w[j] = exp_nonpos((x - m) * rc.inv_t);
       s = s + w[j];
     }
   }
@@ -425,13 +448,13 @@ __device__ __forceinline__ void sample_tail(const Params& p, const uint64_t (&v)
       acc = acc + pr[j];
       c[j] = acc;
       const int idx = base + j;
-      if (idx >= 1 && my_drop == K && !((c[j] - pr[j]) < p.top_p_f)) my_drop = idx;
+      if (idx >= 1 && my_drop == K && !((c[j] - pr[j]) < rc.top_p)) my_drop = idx;
     }
   }
   // lanes hold consecutive rank ranges, so the lowest lane with a hit has the first hit
   const uint64_t drops = __ballot(my_drop < K);
   const int first_drop = drops ? __builtin_amdgcn_readlane(my_drop, __builtin_ctzll(drops)) : K;
-  const int r = (p.keep_all || first_drop == K) ? K - 1 : first_drop - 1;
+  const int r = (rc.keep_all || first_drop == K) ? K - 1 : first_drop - 1;
   float mine_c = 0.0f;
 #pragma unroll
   for (int j = 0; j < RB; ++j)
@@ -460,13 +483,18 @@ __device__ __forceinline__ void sample_tail(const Params& p, const uint64_t (&v)
   }
   if (l == 0) p.out[row] = (int64_t)(0xFFFFFFFFu - lo32);
   if (p.keep != nullptr) {
+    const size_t rowo = (size_t)row * p.K;  // rows of the outputs are the call's K wide
 #pragma unroll
     for (int j = 0; j < RB; ++j) {
       const int idx = base + j;
       if (j < R && idx < K) {
-        p.keep[(size_t)row * K + idx] = (uint8_t)(idx <= r);
-        p.renormed[(size_t)row * K + idx] = idx <= r ? pr[j] / zp : 0.0f;
+        p.keep[rowo + idx] = (uint8_t)(idx <= r);
+        p.renormed[rowo + idx] = idx <= r ? pr[j] / zp : 0.0f;
       }
+    }
+    for (int idx = K + l; idx < p.K; idx += 64) {  // ranks past the row's own k
+      p.keep[rowo + idx] = 0;
+      p.renormed[rowo + idx] = 0.0f;
     }
   }
 }
@@ -476,7 +504,7 @@ __device__ __forceinline__ void sample_tail(const Params& p, const uint64_t (&v)
 // R = ceil(K/64); when R < RB they are re-laid out through top[].
 template <int RB>
 __device__ __forceinline__ void wave_finish(const Params& p, uint64_t (&v)[RB], uint64_t* top, int row,
-                            float u) {
+                            const RowCtl& rc) {
   const int l = lane_id();
   const int K = p.K;
   if (p.ids != nullptr) {
@@ -487,7 +515,8 @@ __device__ __forceinline__ void wave_finish(const Params& p, uint64_t (&v)[RB], 
     }
     return;
   }
-  const int R = (K + 63) >> 6;
+  advance_offset(p);
+  const int R = (rc.k + 63) >> 6;
   if (R != RB) {
 #pragma unroll
     for (int i = 0; i < RB; ++i) {
@@ -498,10 +527,10 @@ __device__ __forceinline__ void wave_finish(const Params& p, uint64_t (&v)[RB], 
 #pragma unroll
     for (int j = 0; j < RB; ++j) {
       const int e = l * R + j;
-      v[j] = (j < R && e < K) ? top[e] : 0ull;
+      v[j] = (j < R && e < rc.k) ? top[e] : 0ull;
     }
   }
-  sample_tail<RB, false>(p, v, top, K, row, u);
+  sample_tail<RB, false>(p, v, top, rc, row);
 }
 
 // ---- the kernel ----------------------------------------------------------------------------
@@ -574,17 +603,17 @@ __device__ __forceinline__ uint32_t key_at(const uint32_t (&k)[4], int j) {
 template <int RB, int NT>
 __device__ __forceinline__ void wave_back_wide(const Params& p, Smem<NT>& sm, int keff, int ncand,
                                                bool sorted_in_lds, bool regions, int row,
-                                               int split, float u_row);
+                                               int split, const RowCtl& rc);
 
 template <int RB, int NT>
 __device__ __forceinline__ void wave_tail_regs(const Params& p, Smem<NT>& sm, uint64_t (&v)[RB],
-                                               int keff, int row, int split, float u_row);
+                                               int keff, int row, int split, const RowCtl& rc);
 
 template <int RB, int NT>
 __device__ __forceinline__ void wave_back(const Params& p, Smem<NT>& sm, int keff, int ncand, bool sorted_in_lds,
-                          bool regions, int row, int split, float u_row) {
+                          bool regions, int row, int split, const RowCtl& rc) {
   if constexpr (RB > 4) {
-    wave_back_wide<RB, NT>(p, sm, keff, ncand, sorted_in_lds, regions, row, split, u_row);
+    wave_back_wide<RB, NT>(p, sm, keff, ncand, sorted_in_lds, regions, row, split, rc);
     return;
   }
   const int l = lane_id();
@@ -621,14 +650,14 @@ __device__ __forceinline__ void wave_back(const Params& p, Smem<NT>& sm, int kef
 #pragma unroll
     for (int i = 0; i < RB; ++i) v[i] = 0ull;
   }
-  wave_tail_regs<RB, NT>(p, sm, v, keff, row, split, u_row);
+  wave_tail_regs<RB, NT>(p, sm, v, keff, row, split, rc);
 }
 
 // Wave 0 with the slice's sorted top keff in v[] (blocked by RB, zeros past keff): probe stop,
 // split hand-off and row merge when S > 1, then the ids or the sampling tail.
 template <int RB, int NT>
 __device__ __forceinline__ void wave_tail_regs(const Params& p, Smem<NT>& sm, uint64_t (&v)[RB],
-                                               int keff, int row, int split, float u_row) {
+                                               int keff, int row, int split, const RowCtl& rc) {
   const int l = lane_id();
   FSAMP_TRACE(5);
   if (p.stop == 4) {
@@ -681,7 +710,7 @@ __device__ __forceinline__ void wave_tail_regs(const Params& p, Smem<NT>& sm, ui
     return;
   }
   // 7. candidate ids, or the sampling tail
-  wave_finish<RB>(p, v, sm.top, row, u_row);
+  wave_finish<RB>(p, v, sm.top, row, rc);
   FSAMP_TRACE(9);
   FSAMP_RTRACE(1);
 }
@@ -691,7 +720,7 @@ __device__ __forceinline__ void wave_tail_regs(const Params& p, Smem<NT>& sm, ui
 template <int RB, int NT>
 __device__ __forceinline__ void wave_back_wide(const Params& p, Smem<NT>& sm, int keff, int ncand,
                                                bool sorted_in_lds, bool regions, int row,
-                                               int split, float u_row) {
+                                               int split, const RowCtl& rc) {
   const int l = lane_id();
   if (keff > 0 && !sorted_in_lds) {
     const uint64_t* base = regions ? sm.top : sm.g.cand;
@@ -743,8 +772,9 @@ __device__ __forceinline__ void wave_back_wide(const Params& p, Smem<NT>& sm, in
     for (int i = l; i < p.K; i += 64) p.ids[(size_t)row * p.K + i] = (int64_t)unpack_id(sm.top[i]);
     return;
   }
+  advance_offset(p);
   const uint64_t none[RB] = {};
-  sample_tail<RB, true>(p, none, sm.top, p.K, row, u_row);
+  sample_tail<RB, true>(p, none, sm.top, rc, row);
   FSAMP_TRACE(9);
   FSAMP_RTRACE(1);
 }
@@ -781,8 +811,31 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
   const int keff = min(p.K, count);
   FSAMP_TRACE(0);
   FSAMP_RTRACE(0);
-  // the row's uniform, fetched now so that its latency hides under the slice loads
-  const float u_row = p.u != nullptr ? p.u[row] : rng_uniform(p.seed, p.offset, (uint32_t)row);
+  // the row's uniform and controls, fetched now so that their latency hides under the loads
+  RowCtl rc;
+  if (p.u != nullptr) {
+    rc.u = p.u[row];
+  } else {
+    const uint64_t off = p.offset_ctr != nullptr
+                             ? __hip_atomic_load(p.offset_ctr, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT)
+                             : p.offset;
+    rc.u = rng_uniform(p.seed, off, (uint32_t)row);
+  }
+  rc.k = p.K;
+  rc.top_p = p.top_p_f;
+  rc.keep_all = p.keep_all;
+  rc.inv_t = 1.0f;
+  if (p.topk_row != nullptr) rc.k = min(max(p.topk_row[row], 1), p.K);
+  if (p.topp_row != nullptr) {
+    rc.top_p = p.topp_row[row];
+    rc.keep_all = rc.top_p >= 1.0f ? 1 : 0;
+  }
+  if (p.temp_row != nullptr) {
+    const float T = p.temp_row[row];
+    if (T > 0.0f) rc.inv_t = 1.0f / T;
+    else rc.k = 1;  // temperature <= 0 (or NaN): greedy
+  }
   if (t == 0) sm.misc[M_CNT] = 0;
 
   // 1. load the slice into registers as packed keys (padding = key 0).  With VEC, V and the
@@ -1123,11 +1176,11 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
 
   // From here on wave 0 carries the workgroup alone: no more workgroup barriers.
   if (wid != 0) return;
-  if (p.K <= 64) wave_back<1, NT>(p, sm, keff, ncand, sorted_in_lds, regions, row, split, u_row);
-  else if (p.K <= 128) wave_back<2, NT>(p, sm, keff, ncand, sorted_in_lds, regions, row, split, u_row);
-  else if (p.K <= 256) wave_back<4, NT>(p, sm, keff, ncand, sorted_in_lds, regions, row, split, u_row);
-  else if (p.K <= 512) wave_back<8, NT>(p, sm, keff, ncand, sorted_in_lds, regions, row, split, u_row);
-  else wave_back<16, NT>(p, sm, keff, ncand, sorted_in_lds, regions, row, split, u_row);
+  if (p.K <= 64) wave_back<1, NT>(p, sm, keff, ncand, sorted_in_lds, regions, row, split, rc);
+  else if (p.K <= 128) wave_back<2, NT>(p, sm, keff, ncand, sorted_in_lds, regions, row, split, rc);
+  else if (p.K <= 256) wave_back<4, NT>(p, sm, keff, ncand, sorted_in_lds, regions, row, split, rc);
+  else if (p.K <= 512) wave_back<8, NT>(p, sm, keff, ncand, sorted_in_lds, regions, row, split, rc);
+  else wave_back<16, NT>(p, sm, keff, ncand, sorted_in_lds, regions, row, split, rc);
 }
 
 // ---- instantiation table -----------------------------------------------------------------------

@@ -8,11 +8,18 @@ there is no other implementation behind these functions.
 
 Deliberate differences from the reference:
   - top_k may be up to 1024 (reference: 128), so the "top_k must be <= ..." message names 1024;
-  - ``offset < 0`` (torch-generator path, csrc/fused_sampling.cu:441-447) takes the seed and
-    offset from torch's default generator of the logits' device on the host and advances that
-    generator's offset by 4 per call, as the reference's philox_cuda_state(4) does; the device
-    stream is splitmix64(seed, offset, row) like the explicit-offset path.  Under HIP-graph
-    capture this path raises: pass an explicit offset or ``u`` there.
+  - ``offset < 0`` (torch-generator path, csrc/fused_sampling.cu:441-447): outside graph
+    capture the seed and offset come from torch's default generator of the logits' device, on
+    the host, and the generator's offset advances by 4 per call, as the reference's
+    philox_cuda_state(4) does.  Under HIP-graph capture the offset comes from a device counter
+    that the kernel itself advances by 4 per call, so every replay draws fresh uniforms (the
+    reference reads a graph-safe device offset for the same purpose, :112-118).  The counter is
+    created, from the generator's offset, by the first generator-path call made outside
+    capture (a warm-up call, as graph capture needs anyway).  Either way the row uniform is
+    splitmix64(seed, offset, row) like the explicit-offset path.
+
+Extensions with no counterpart in the reference (SEMANTICS.md lists them as open):
+``sample_fused_ex`` with per-row top_k / top_p / temperature.
 """
 
 from __future__ import annotations
@@ -24,6 +31,7 @@ import torch
 from . import _lib
 
 _WORKSPACES: dict = {}
+_OFFSET_COUNTERS: dict = {}  # device index -> int64[1] device tensor (graph-safe draw offset)
 
 
 def _stream_ptr(device: torch.device) -> int:
@@ -66,12 +74,12 @@ def make_plan(logits: torch.Tensor, top_k: int, splits_override: int = 0) -> _li
 
 
 def _workspace(logits: torch.Tensor, top_k: int, splits_override: int, stream: int):
-    """Cached per (device, stream) workspace whose per-row counters are zero.
+    """Cached per (device, stream) workspace whose counters are zero.
 
-    Layout (include/fsamp.h): [counters: round_up(128*B, 256) bytes][per-split candidates].
-    A call with S > 1 leaves its counters zero and candidates behind them; a later call with a
-    larger B would read those candidates as counters, so the buffer is zeroed again whenever
-    the counter region grows past what is known to be clean.
+    Layout (include/fsamp.h): [row counters: round_up(128*B, 256) bytes][grid counter: 256]
+    [per-split candidates].  A call leaves its counters zero and candidates behind them; a
+    later call with a larger B would read those candidates as counters, so the buffer is zeroed
+    again whenever the counter region grows past what is known to be clean.
     """
     lib = _lib.load()
     B, V = logits.shape
@@ -81,7 +89,7 @@ def _workspace(logits: torch.Tensor, top_k: int, splits_override: int, stream: i
         return None, 0
     key = (logits.device.index, stream)
     entry = _WORKSPACES.get(key)
-    counter_bytes = ((128 * B + 255) // 256) * 256
+    counter_bytes = ((128 * B + 255) // 256) * 256 + 256
     if entry is None or entry["buf"].numel() < need:
         buf = torch.empty(max(need, 1 << 20), dtype=torch.uint8, device=logits.device)
         _lib.check(lib.fsamp_workspace_init(ctypes.c_void_p(buf.data_ptr()), buf.numel(),
@@ -102,15 +110,35 @@ def _ws_args(logits, top_k, splits_override, stream):
     return (ctypes.c_void_p(buf.data_ptr()) if buf is not None else None), nbytes
 
 
-def _generator_seed_offset(device: torch.device) -> tuple[int, int]:
-    if torch.cuda.is_current_stream_capturing():
-        raise RuntimeError("the torch-generator draw (offset < 0) cannot be captured in a HIP "
-                           "graph; pass an explicit offset or per-row u")
+def _generator(device: torch.device):
     idx = device.index if device.index is not None else torch.cuda.current_device()
-    gen = torch.cuda.default_generators[idx]
+    return idx, torch.cuda.default_generators[idx]
+
+
+def offset_counter(device: torch.device) -> torch.Tensor:
+    """The device's graph-safe offset counter (int64[1]); created from torch's generator offset
+    on first use, which must happen outside graph capture."""
+    idx, gen = _generator(device)
+    ctr = _OFFSET_COUNTERS.get(idx)
+    if ctr is None:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("call sample_fused with offset=None once outside graph capture "
+                               "before capturing it (that creates its device offset counter)")
+        ctr = torch.tensor([gen.get_offset()], dtype=torch.int64, device=torch.device("cuda", idx))
+        _OFFSET_COUNTERS[idx] = ctr
+    return ctr
+
+
+def _generator_draw(device: torch.device):
+    """(seed, offset, counter): outside capture the host generator's offset (advanced by 4) and
+    no counter; under capture the device counter, which the kernel advances."""
+    idx, gen = _generator(device)
+    if torch.cuda.is_current_stream_capturing():
+        return gen.initial_seed(), 0, offset_counter(device)
+    offset_counter(device)  # make sure a later capture finds it
     seed, off = gen.initial_seed(), gen.get_offset()
     gen.set_offset(off + 4)
-    return seed, off
+    return seed, off, None
 
 
 def _u_ptr(u: torch.Tensor | None, B: int, device: torch.device):
@@ -122,35 +150,50 @@ def _u_ptr(u: torch.Tensor | None, B: int, device: torch.device):
     return ctypes.c_void_p(u.data_ptr())
 
 
-def _sample(logits, top_k, top_p, seed, offset, splits_override, u, stages):
+def _row_array(a, B: int, dtype: torch.dtype, device: torch.device, name: str):
+    if a is None:
+        return None
+    if not (isinstance(a, torch.Tensor) and a.is_cuda and a.dtype == dtype and a.is_contiguous()
+            and a.numel() == B and a.device == device):
+        raise RuntimeError(f"{name} must be a contiguous {dtype} cuda tensor with one value per "
+                           "row")
+    return a
+
+
+def _sample(logits, top_k, top_p, seed, offset, splits_override, u, stages, top_k_row=None,
+            top_p_row=None, temperature=None):
     dtype = _check_logits(logits)
     B, V = logits.shape
     _check_top_k(int(top_k), V)
     _check_top_p(float(top_p))
+    counter = None
     if u is None and offset < 0:
-        seed, offset = _generator_seed_offset(logits.device)
-    stream = _stream_ptr(logits.device)
+        seed, offset, counter = _generator_draw(logits.device)
+    dev = logits.device
+    kr = _row_array(top_k_row, B, torch.int32, dev, "top_k_row")
+    pr = _row_array(top_p_row, B, torch.float32, dev, "top_p_row")
+    tr = _row_array(temperature, B, torch.float32, dev, "temperature")
+    rows = _lib.RowParams(kr.data_ptr() if kr is not None else None,
+                          pr.data_ptr() if pr is not None else None,
+                          tr.data_ptr() if tr is not None else None,
+                          counter.data_ptr() if counter is not None else None)
+    stream = _stream_ptr(dev)
     ws, ws_bytes = _ws_args(logits, top_k, splits_override, stream)
-    out = torch.empty(B, dtype=torch.int64, device=logits.device)
-    uptr = _u_ptr(u, B, logits.device)
-    lib = _lib.load()
+    out = torch.empty(B, dtype=torch.int64, device=dev)
+    uptr = _u_ptr(u, B, dev)
     seed64, off64 = int(seed) & (2**64 - 1), int(offset) & (2**64 - 1)
+    keep = renormed = None
     if stages:
         K = min(int(top_k), V)
-        keep = torch.empty((B, K), dtype=torch.bool, device=logits.device)
-        renormed = torch.empty((B, K), dtype=torch.float32, device=logits.device)
-        _lib.check(lib.fsamp_stages(ctypes.c_void_p(logits.data_ptr()), dtype, B, V, int(top_k),
-                                    float(top_p), uptr, seed64, off64,
-                                    ctypes.c_void_p(out.data_ptr()),
-                                    ctypes.c_void_p(keep.data_ptr()),
-                                    ctypes.c_void_p(renormed.data_ptr()), ws, ws_bytes,
-                                    int(splits_override), ctypes.c_void_p(stream)))
-        return [out, keep, renormed]
-    _lib.check(lib.fsamp_sample(ctypes.c_void_p(logits.data_ptr()), dtype, B, V, int(top_k),
-                                float(top_p), uptr, seed64, off64,
-                                ctypes.c_void_p(out.data_ptr()), ws, ws_bytes,
-                                int(splits_override), ctypes.c_void_p(stream)))
-    return out
+        keep = torch.empty((B, K), dtype=torch.bool, device=dev)
+        renormed = torch.empty((B, K), dtype=torch.float32, device=dev)
+    _lib.check(_lib.load().fsamp_sample_ex(
+        ctypes.c_void_p(logits.data_ptr()), dtype, B, V, int(top_k), float(top_p), uptr, seed64,
+        off64, ctypes.byref(rows), ctypes.c_void_p(out.data_ptr()),
+        ctypes.c_void_p(keep.data_ptr()) if stages else None,
+        ctypes.c_void_p(renormed.data_ptr()) if stages else None, ws, ws_bytes,
+        int(splits_override), ctypes.c_void_p(stream)))
+    return [out, keep, renormed] if stages else out
 
 
 def sample_fused(logits: torch.Tensor, top_k: int, top_p: float, seed: int, offset: int,
@@ -158,7 +201,7 @@ def sample_fused(logits: torch.Tensor, top_k: int, top_p: float, seed: int, offs
     """[B, V] logits -> [B] int64 token ids (csrc/fused_sampling.cu:449-458).
 
     offset >= 0: row b's uniform is splitmix64(seed, offset, b); offset < 0: seed and offset
-    come from torch's default generator, which is advanced.
+    come from torch's default generator, which is advanced (a device counter under capture).
     """
     return _sample(logits, top_k, top_p, seed, offset, splits_override, None, False)
 
@@ -181,6 +224,17 @@ def stages_fused_u(logits: torch.Tensor, top_k: int, top_p: float, u: torch.Tens
                    splits_override: int = 0) -> list:
     """stages_fused with explicit per-row uniforms."""
     return _sample(logits, top_k, top_p, 0, 0, splits_override, u, True)
+
+
+def sample_fused_ex(logits: torch.Tensor, top_k: int, top_p: float, *, u=None, seed: int = 0,
+                    offset: int = -1, top_k_row=None, top_p_row=None, temperature=None,
+                    splits_override: int = 0, stages: bool = False):
+    """Sampling with per-row controls (fsamp_sample_ex): top_k_row int32[B] (row b samples from
+    its top min(max(top_k_row[b], 1), top_k) ranks), top_p_row float32[B], temperature
+    float32[B] (softmax of (x - max) / T; T <= 0 is greedy).  u, or seed / offset as in
+    sample_fused.  Returns token ids, or [token ids, keep, renormed] with stages=True."""
+    return _sample(logits, top_k, top_p, seed, offset, splits_override, u, stages,
+                   top_k_row, top_p_row, temperature)
 
 
 def topk_fused(logits: torch.Tensor, top_k: int, splits_override: int) -> torch.Tensor:

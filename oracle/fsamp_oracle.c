@@ -223,13 +223,15 @@ static void lane_scan(float* v) {
   memcpy(v, nxt, sizeof(nxt));
 }
 
-/* x: K candidate values, descending.  Writes w (scratch), p, c; returns r and pick. */
-static tail_out_t tail_f32(const float* x, int K, double top_p, float u, float* w, float* p,
-                           float* c) {
+/* x: K candidate values, descending.  Writes w (scratch), p, c; returns r and pick.
+ * inv_t scales the shifted logits before exp, (x_j - m) * inv_t in fp32 (1 / temperature;
+ * exactly 1 without a temperature, which leaves x_j - m unchanged). */
+static tail_out_t tail_f32(const float* x, int K, double top_p, float u, float inv_t, float* w,
+                           float* p, float* c) {
   const int R = (K + OR_LANES - 1) / OR_LANES;
   float lane_s[OR_LANES];
   const float m = x[0];
-  for (int j = 0; j < K; ++j) w[j] = oracle_expf(x[j] - m);
+  for (int j = 0; j < K; ++j) w[j] = oracle_expf((x[j] - m) * inv_t);
 
   /* z: per-lane serial sums, combined by the lane scan; z is its last lane */
   for (int l = 0; l < OR_LANES; ++l) {
@@ -293,10 +295,20 @@ static tail_out_t tail_f32(const float* x, int K, double top_p, float u, float* 
  *   cutoff [B] int32 = number of kept ranks.
  * Returns OR_OK or OR_BADARG / OR_NOMEM.  Does not validate values (see oracle_validate).
  */
-int oracle_sample(const void* logits, int dtype, int64_t B, int64_t V, int64_t top_k,
-                  double top_p, const float* u, int64_t* token_ids, int64_t* topk_ids,
-                  float* topk_vals, float* probs, float* cumsum, uint8_t* keep,
-                  float* renormed, int32_t* cutoff, int nthreads) {
+/*
+ * oracle_sample_rows: oracle_sample with per-row controls (each array NULL or [B]), the
+ * semantics of fsamp_sample_ex (include/fsamp.h):
+ *   topk_row[b]  row b uses the first min(max(topk_row[b], 1), K) ranks of the top-K
+ *   topp_row[b]  row b's threshold (fp32); >= 1 keeps every rank of the row
+ *   temp_row[b]  inv_t = 1.0f / temp_row[b] scales (x - max) before exp; <= 0 or NaN: greedy
+ * Stage outputs stay [B, K] with K = min(top_k, V); ranks past a row's own k are 0, and
+ * probs / cumsum there are 0 as well.
+ */
+int oracle_sample_rows(const void* logits, int dtype, int64_t B, int64_t V, int64_t top_k,
+                       double top_p, const float* u, const int32_t* topk_row,
+                       const float* topp_row, const float* temp_row, int64_t* token_ids,
+                       int64_t* topk_ids, float* topk_vals, float* probs, float* cumsum,
+                       uint8_t* keep, float* renormed, int32_t* cutoff, int nthreads) {
   if (B < 0 || V < 1 || top_k < 1 || !(top_p > 0.0 && top_p <= 1.0) || u == NULL ||
       token_ids == NULL || (dtype != OR_F16 && dtype != OR_BF16 && dtype != OR_F32))
     return OR_BADARG;
@@ -326,17 +338,27 @@ int oracle_sample(const void* logits, int dtype, int64_t B, int64_t V, int64_t t
       float* w = x + K;
       float* p = x + 2 * K;
       float* c = x + 3 * K;
-      const tail_out_t o = tail_f32(x, (int)K, top_p, u[b], w, p, c);
+      int64_t kr = K;
+      double pr = top_p;
+      float inv_t = 1.0f;
+      if (topk_row) kr = topk_row[b] < 1 ? 1 : (topk_row[b] > K ? K : topk_row[b]);
+      if (topp_row) pr = (double)topp_row[b];
+      if (temp_row) {
+        if (temp_row[b] > 0.0f) inv_t = 1.0f / temp_row[b];
+        else kr = 1;
+      }
+      const tail_out_t o = tail_f32(x, (int)kr, pr, u[b], inv_t, w, p, c);
       token_ids[b] = order[o.pick];
       const float zp = c[o.r];
       for (int64_t j = 0; j < K; ++j) {
         const int64_t at = b * K + j;
+        const int in = j < kr;
         if (topk_ids) topk_ids[at] = order[j];
         if (topk_vals) topk_vals[at] = x[j];
-        if (probs) probs[at] = p[j];
-        if (cumsum) cumsum[at] = c[j];
-        if (keep) keep[at] = (uint8_t)(j <= o.r);
-        if (renormed) renormed[at] = j <= o.r ? p[j] / zp : 0.0f;
+        if (probs) probs[at] = in ? p[j] : 0.0f;
+        if (cumsum) cumsum[at] = in ? c[j] : 0.0f;
+        if (keep) keep[at] = (uint8_t)(in && j <= o.r);
+        if (renormed) renormed[at] = in && j <= o.r ? p[j] / zp : 0.0f;
       }
       if (cutoff) cutoff[b] = (int32_t)(o.r + 1);
     }
@@ -348,14 +370,22 @@ int oracle_sample(const void* logits, int dtype, int64_t B, int64_t V, int64_t t
   return status;
 }
 
+int oracle_sample(const void* logits, int dtype, int64_t B, int64_t V, int64_t top_k,
+                  double top_p, const float* u, int64_t* token_ids, int64_t* topk_ids,
+                  float* topk_vals, float* probs, float* cumsum, uint8_t* keep,
+                  float* renormed, int32_t* cutoff, int nthreads) {
+  return oracle_sample_rows(logits, dtype, B, V, top_k, top_p, u, NULL, NULL, NULL, token_ids,
+                            topk_ids, topk_vals, probs, cumsum, keep, renormed, cutoff, nthreads);
+}
+
 /*
  * oracle_stages_f64: the same pipeline in double precision (softmax, cumsum, cut, renorm),
  * the yardstick the fp32 restatement and the GPU are held to.  topk selection is shared with
  * oracle_sample (integer work, no rounding).  Outputs [B,K] doubles; cutoff [B].
  */
-int oracle_stages_f64(const void* logits, int dtype, int64_t B, int64_t V, int64_t top_k,
-                      double top_p, double* probs, double* cumsum, double* renormed,
-                      int32_t* cutoff) {
+int oracle_stages_f64_t(const void* logits, int dtype, int64_t B, int64_t V, int64_t top_k,
+                        double top_p, double temperature, double* probs, double* cumsum,
+                        double* renormed, int32_t* cutoff) {
   if (B < 0 || V < 1 || top_k < 1 || !(top_p > 0.0 && top_p <= 1.0) ||
       (dtype != OR_F16 && dtype != OR_BF16 && dtype != OR_F32))
     return OR_BADARG;
@@ -385,7 +415,7 @@ int oracle_stages_f64(const void* logits, int dtype, int64_t B, int64_t V, int64
     double* c = cumsum + b * K;
     double z = 0.0;
     for (int64_t j = 0; j < K; ++j) {
-      p[j] = exp(x[j] - x[0]);
+      p[j] = exp((x[j] - x[0]) / temperature);
       z += p[j];
     }
     double acc = 0.0;
@@ -411,6 +441,13 @@ int oracle_stages_f64(const void* logits, int dtype, int64_t B, int64_t V, int64
   free(tmp);
   free(x);
   return OR_OK;
+}
+
+int oracle_stages_f64(const void* logits, int dtype, int64_t B, int64_t V, int64_t top_k,
+                      double top_p, double* probs, double* cumsum, double* renormed,
+                      int32_t* cutoff) {
+  return oracle_stages_f64_t(logits, dtype, B, V, top_k, top_p, 1.0, probs, cumsum, renormed,
+                             cutoff);
 }
 
 /* ---- array helpers for the tests ---------------------------------------------------------- */

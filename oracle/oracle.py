@@ -41,8 +41,13 @@ def lib():
         L.oracle_sample.argtypes = [vp, i32, i64, i64, i64, dbl, vp, vp, vp, vp, vp, vp, vp, vp,
                                     vp, i32]
         L.oracle_sample.restype = i32
+        L.oracle_sample_rows.argtypes = [vp, i32, i64, i64, i64, dbl, vp, vp, vp, vp, vp, vp, vp,
+                                         vp, vp, vp, vp, vp, i32]
+        L.oracle_sample_rows.restype = i32
         L.oracle_stages_f64.argtypes = [vp, i32, i64, i64, i64, dbl, vp, vp, vp, vp]
         L.oracle_stages_f64.restype = i32
+        L.oracle_stages_f64_t.argtypes = [vp, i32, i64, i64, i64, dbl, dbl, vp, vp, vp, vp]
+        L.oracle_stages_f64_t.restype = i32
         L.oracle_validate.argtypes = [vp, i32, i64, i64]
         L.oracle_validate.restype = i32
         L.oracle_expf_array.argtypes = [vp, vp, i64]
@@ -97,8 +102,12 @@ def validate(x: np.ndarray, dtype: str) -> None:
 
 
 def sample(x: np.ndarray, dtype: str, top_k: int, top_p: float, u: np.ndarray, *,
-           check_inputs: bool = True, return_stages: bool = False, nthreads: int = 1):
-    """The restated sampler: [B,V] logits + u[B] -> token ids [B] (or Stages)."""
+           check_inputs: bool = True, return_stages: bool = False, nthreads: int = 1,
+           top_k_row=None, top_p_row=None, temperature=None):
+    """The restated sampler: [B,V] logits + u[B] -> token ids [B] (or Stages).
+
+    top_k_row (int32 [B]), top_p_row (float32 [B]) and temperature (float32 [B]) are the
+    per-row controls of fsamp_sample_ex (oracle_sample_rows)."""
     x = _logits(x, dtype)
     if top_k < 1:
         raise ValueError(f"top_k must be >= 1, got {top_k}")
@@ -117,9 +126,13 @@ def sample(x: np.ndarray, dtype: str, top_k: int, top_p: float, u: np.ndarray, *
         cutoff = np.empty(B, np.int32)
     else:
         ids = vals = probs = cum = ren = keep = cutoff = None
-    rc = lib().oracle_sample(_ptr(x), DTYPES[dtype], B, V, int(top_k), float(top_p), _ptr(u),
-                             _ptr(tok), _ptr(ids), _ptr(vals), _ptr(probs), _ptr(cum),
-                             _ptr(keep), _ptr(ren), _ptr(cutoff), int(nthreads))
+    rows = [None if a is None else np.ascontiguousarray(a, dtype=t).reshape(B)
+            for a, t in ((top_k_row, np.int32), (top_p_row, np.float32),
+                         (temperature, np.float32))]
+    rc = lib().oracle_sample_rows(_ptr(x), DTYPES[dtype], B, V, int(top_k), float(top_p),
+                                  _ptr(u), _ptr(rows[0]), _ptr(rows[1]), _ptr(rows[2]),
+                                  _ptr(tok), _ptr(ids), _ptr(vals), _ptr(probs), _ptr(cum),
+                                  _ptr(keep), _ptr(ren), _ptr(cutoff), int(nthreads))
     if rc != 0:
         raise RuntimeError(f"oracle_sample failed ({rc})")
     if not return_stages:
@@ -127,8 +140,9 @@ def sample(x: np.ndarray, dtype: str, top_k: int, top_p: float, u: np.ndarray, *
     return Stages(ids, vals, probs, cum, keep.astype(bool), cutoff, ren, tok)
 
 
-def stages_f64(x: np.ndarray, dtype: str, top_k: int, top_p: float):
-    """fp64 restatement of softmax/cumsum/cut/renorm over the same top-k candidates.
+def stages_f64(x: np.ndarray, dtype: str, top_k: int, top_p: float, temperature: float = 1.0):
+    """fp64 restatement of softmax/cumsum/cut/renorm over the same top-k candidates, with the
+    softmax taken over (x - max) / temperature.
 
     Returns (probs, cumsum, renormed, cutoff) as float64 [B,K] arrays and int32 [B].
     """
@@ -137,8 +151,9 @@ def stages_f64(x: np.ndarray, dtype: str, top_k: int, top_p: float):
     K = min(int(top_k), V)
     probs, cum, ren = (np.empty((B, K), np.float64) for _ in range(3))
     cutoff = np.empty(B, np.int32)
-    rc = lib().oracle_stages_f64(_ptr(x), DTYPES[dtype], B, V, int(top_k), float(top_p),
-                                 _ptr(probs), _ptr(cum), _ptr(ren), _ptr(cutoff))
+    rc = lib().oracle_stages_f64_t(_ptr(x), DTYPES[dtype], B, V, int(top_k), float(top_p),
+                                   float(temperature), _ptr(probs), _ptr(cum), _ptr(ren),
+                                   _ptr(cutoff))
     if rc != 0:
         raise RuntimeError(f"oracle_stages_f64 failed ({rc})")
     return probs, cum, ren, cutoff

@@ -51,7 +51,7 @@ def test_plans_for_the_benchmark_shapes(B, V, k, S, threads):
     assert rc == 0 and p.splits == S and p.threads == threads
     assert p.threads * p.chunks * 8 >= p.slice and p.slice * p.splits >= V
     assert p.slice % 8 == 0 and p.vec == 1
-    assert p.workspace_bytes == (0 if S == 1 else ((128 * B + 255) // 256) * 256 + B * S * k * 8)
+    assert p.workspace_bytes == ((128 * B + 255) // 256) * 256 + 256 + (0 if S == 1 else B * S * k * 8)
 
 
 def test_every_plan_tiles_its_slice_and_fits_the_merge_buffer():

@@ -459,3 +459,129 @@ def test_wave_primitives_have_the_lane_layouts_the_kernel_assumes():
     hi = (lanes * 21) & 63
     order = np.argsort(-hi.astype(np.int64), kind="stable")
     assert np.array_equal(got[10], hi[order]) and np.array_equal(got[11], 0xFFFFFFFF - lanes[order])
+
+
+# --- per-row top_k / top_p / temperature (fsamp_sample_ex) -------------------------------------
+
+def _row_controls(B, K, seed):
+    g = np.random.Generator(np.random.PCG64(seed))
+    ks = g.integers(1, K + 1, B).astype(np.int32)
+    ks[:4] = [1, K, 0, K + 7][:min(4, B)]  # clamped to [1, K]
+    ps = g.uniform(0.05, 1.0, B).astype(np.float32)
+    ps[4:8] = [1.0, 1.5, 0.0, 0.999][:max(0, min(4, B - 4))]
+    ts = g.uniform(0.3, 3.0, B).astype(np.float32)
+    ts[8:12] = [1.0, 0.0, -2.0, 0.05][:max(0, min(4, B - 8))]
+    return ks, ps, ts
+
+
+@pytest.mark.parametrize("B,V,K,dtype", [(16, 151936, 50, "bfloat16"),   # split rows
+                                         (40, 32000, 100, "float16"),    # one workgroup per row
+                                         (12, 151936, 1024, "bfloat16"),  # wide k, LDS tail
+                                         (12, 20000, 300, "bfloat16")])  # k in (256, 512]
+def test_per_row_controls_match_the_oracle_bit_for_bit(B, V, K, dtype):
+    bits = randn_bits((B, V), 7000 + K, 3.0, dtype)
+    x = dev(bits, dtype)
+    un = ustream(B, 7100 + K)
+    ks, ps, ts = _row_controls(B, K, 7200 + K)
+    tok, keep, ren = fused_sampling.sample_fused_ex(
+        x, K, 0.9, u=torch.from_numpy(un).cuda(), top_k_row=torch.from_numpy(ks).cuda(),
+        top_p_row=torch.from_numpy(ps).cuda(), temperature=torch.from_numpy(ts).cuda(),
+        stages=True)
+    want = O.sample(bits, dtype, K, 0.9, un, return_stages=True, nthreads=8, top_k_row=ks,
+                    top_p_row=ps, temperature=ts)
+    assert np.array_equal(tok.cpu().numpy(), want.token_ids)
+    assert np.array_equal(keep.cpu().numpy(), want.keep)
+    assert np.array_equal(ren.cpu().numpy(), want.renormed)
+    # and the plain entry agrees with the per-row entry when every row carries the call's values
+    same = fused_sampling.sample_fused_ex(
+        x, K, 0.9, u=torch.from_numpy(un).cuda(),
+        top_k_row=torch.full((B,), K, dtype=torch.int32, device="cuda"),
+        top_p_row=torch.full((B,), 0.9, dtype=torch.float32, device="cuda"),
+        temperature=torch.ones(B, device="cuda"))
+    assert torch.equal(same, fused.sample_fused_u(x, K, 0.9, torch.from_numpy(un).cuda()))
+
+
+def test_greedy_temperature_returns_the_argmax_with_the_lowest_id_tie():
+    bits = randn_bits((8, 5000), 7300, 2.0, "bfloat16")
+    bits[:, 100] = bits[:, 17] = W.to_bits(np.float32([30.0]), "bfloat16")[0]
+    x = dev(bits, "bfloat16")
+    tok = fused_sampling.sample_fused_ex(x, 50, 0.9, u=torch.full((8,), 0.999, device="cuda"),
+                                         temperature=torch.zeros(8, device="cuda"))
+    assert (tok.cpu().numpy() == 17).all()
+
+
+def test_per_row_controls_reject_wrong_arrays():
+    x = dev(randn_bits((4, 1000), 7301, 2.0, "bfloat16"), "bfloat16")
+    with pytest.raises(RuntimeError, match="top_k_row"):
+        fused_sampling.sample_fused_ex(x, 50, 0.9, offset=0,
+                                       top_k_row=torch.ones(4, dtype=torch.int64, device="cuda"))
+    with pytest.raises(RuntimeError, match="temperature"):
+        fused_sampling.sample_fused_ex(x, 50, 0.9, offset=0, temperature=torch.ones(3, device="cuda"))
+
+
+# --- graph-safe generator draw -----------------------------------------------------------------
+
+def _uniforms(seed, offset, B):
+    return O.rng_uniform(seed, offset, B)
+
+
+def test_generator_draw_under_graph_capture_advances_on_every_replay():
+    B = 16
+    bits = randn_bits((B, 6000), 7400, 1.0, "bfloat16")  # flat enough that draws differ
+    x = dev(bits, "bfloat16")
+    torch.manual_seed(2024)
+    fused.sample_fused(x, 50, 0.95)  # warm-up outside capture creates the device counter
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            fused.sample_fused(x, 50, 0.95)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = fused.sample_fused(x, 50, 0.95)
+    ctr = fused_sampling.offset_counter(x.device)
+    seed = torch.cuda.default_generators[0].initial_seed()
+    outs = []
+    for i in range(4):
+        c0 = int(ctr.item())
+        g.replay()
+        torch.cuda.synchronize()
+        assert int(ctr.item()) == c0 + 4, "each replay advances the counter by 4"
+        want = oracle(bits, "bfloat16", 50, 0.95, _uniforms(seed, c0, B)).token_ids
+        got = out.cpu().numpy()
+        assert np.array_equal(got, want)
+        outs.append(got)
+        fused.sample_fused(x, 50, 0.95)  # eager work between replays uses the host generator
+        torch.cuda.synchronize()
+        assert int(ctr.item()) == c0 + 4
+    assert len({o.tobytes() for o in outs}) > 1, "replays draw fresh uniforms"
+
+
+def test_the_device_offset_counter_of_the_c_entry_advances_once_per_call():
+    import ctypes
+    B, V = 64, 30000
+    bits = randn_bits((B, V), 7500, 1.0, "bfloat16")
+    x = dev(bits, "bfloat16")
+    lib = _lib.load()
+    ctr = torch.tensor([1000], dtype=torch.int64, device="cuda")
+    rows = _lib.RowParams(None, None, None, ctr.data_ptr())
+    for splits in (1, 3):
+        for call in range(2):
+            c0 = int(ctr.item())
+            out = torch.empty(B, dtype=torch.int64, device="cuda")
+            stream = fused_sampling._stream_ptr(x.device)
+            ws, wsb = fused_sampling._ws_args(x, 50, splits, stream)
+            _lib.check(lib.fsamp_sample_ex(ctypes.c_void_p(x.data_ptr()), 1, B, V, 50, 0.9, None,
+                                           77, 123456, ctypes.byref(rows),
+                                           ctypes.c_void_p(out.data_ptr()), None, None, ws, wsb,
+                                           splits, ctypes.c_void_p(stream)))
+            torch.cuda.synchronize()
+            assert int(ctr.item()) == c0 + 4
+            want = oracle(bits, "bfloat16", 50, 0.9, _uniforms(77, c0, B)).token_ids
+            assert np.array_equal(out.cpu().numpy(), want)
+    # without a workspace the counter form is refused (it needs the grid counter)
+    assert lib.fsamp_sample_ex(ctypes.c_void_p(x.data_ptr()), 1, B, V, 50, 0.9, None, 77, 0,
+                               ctypes.byref(rows), ctypes.c_void_p(out.data_ptr()), None, None,
+                               None, 0, 1, None) == 6

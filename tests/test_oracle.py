@@ -256,6 +256,94 @@ def test_fp32_stages_track_the_fp64_restatement(name):
     assert (np.abs(zp32 - zp64)[agree] / zp64[agree]).max() < 1e-5
 
 
+# --- per-row controls and temperature (oracle_sample_rows) ------------------------------------
+
+def _rows_case(seed=11, B=12, V=3000, dtype="bfloat16"):
+    x = W.to_bits(randn((B, V), seed, 3.0), dtype)
+    u = np.random.Generator(np.random.PCG64(seed + 1)).random(B, dtype=np.float32)
+    return x, u
+
+
+def test_per_row_k_equals_a_call_with_that_k():
+    x, u = _rows_case()
+    B, K = x.shape[0], 100
+    ks = np.array([1, 2, 7, 50, 63, 64, 65, 99, 100, 100, 200, 0], np.int32)  # clamped to [1, K]
+    got = O.sample(x, "bfloat16", K, 0.9, u, return_stages=True, top_k_row=ks)
+    for b in range(B):
+        kb = int(min(max(ks[b], 1), K))
+        want = O.sample(x[b:b + 1], "bfloat16", kb, 0.9, u[b:b + 1], return_stages=True)
+        assert got.token_ids[b] == want.token_ids[0]
+        assert got.cutoff[b] == want.cutoff[0]
+        assert np.array_equal(got.renormed[b, :kb], want.renormed[0])
+        assert np.array_equal(got.keep[b, :kb], want.keep[0])
+        assert not got.keep[b, kb:].any() and not got.renormed[b, kb:].any()
+
+
+def test_per_row_p_equals_a_call_with_that_p():
+    x, u = _rows_case(seed=21)
+    B = x.shape[0]
+    ps = np.array([0.05, 0.1, 0.3, 0.5, 0.7, 0.9, 0.95, 0.99, 1.0, 1.5, 0.0, -1.0], np.float32)
+    got = O.sample(x, "bfloat16", 50, 0.9, u, return_stages=True, top_p_row=ps)
+    for b in range(B):
+        if ps[b] >= 1.0:
+            pb = 1.0
+        elif ps[b] <= 0.0:
+            # threshold <= 0: only rank 0 survives the exclusive-prefix cut
+            assert got.cutoff[b] == 1 and got.token_ids[b] == got.topk_ids[b, 0]
+            continue
+        else:
+            pb = float(ps[b])
+        want = O.sample(x[b:b + 1], "bfloat16", 50, pb, u[b:b + 1], return_stages=True)
+        assert got.token_ids[b] == want.token_ids[0] and got.cutoff[b] == want.cutoff[0]
+        assert np.array_equal(got.renormed[b], want.renormed[0])
+
+
+def test_temperature_one_is_bit_identical_to_no_temperature():
+    x, u = _rows_case(seed=31)
+    a = O.sample(x, "bfloat16", 64, 0.95, u, return_stages=True)
+    b = O.sample(x, "bfloat16", 64, 0.95, u, return_stages=True,
+                 temperature=np.ones(x.shape[0], np.float32))
+    for f in ("token_ids", "probs", "cumsum", "renormed", "cutoff"):
+        assert np.array_equal(getattr(a, f), getattr(b, f)), f
+
+
+def test_non_positive_temperature_is_greedy():
+    x, u = _rows_case(seed=41)
+    B = x.shape[0]
+    t = np.array([0.0, -1.0, np.nan] * (B // 3), np.float32)
+    s = O.sample(x, "bfloat16", 50, 0.9, np.full(B, 0.999, np.float32), return_stages=True,
+                 temperature=t)
+    assert np.array_equal(s.token_ids, s.topk_ids[:, 0])
+    assert (s.cutoff == 1).all()
+
+
+@pytest.mark.parametrize("temp", [0.25, 0.7, 1.3, 4.0])
+def test_temperature_tracks_the_fp64_restatement(temp):
+    x, u = _rows_case(seed=51, B=16)
+    B = x.shape[0]
+    s = O.sample(x, "bfloat16", 200, 0.95, u, return_stages=True,
+                 temperature=np.full(B, temp, np.float32))
+    p64, c64, r64, cut64 = O.stages_f64(x, "bfloat16", 200, 0.95, temperature=temp)
+    rel = np.abs(s.probs - p64) / np.maximum(p64, 1e-30)
+    assert rel[p64 > 1e-20].max() < 1e-5
+    near = np.abs((c64 - p64) - 0.95) < 1e-6
+    agree = s.cutoff == cut64
+    assert (agree | near.any(-1)).all()
+    zp32 = s.cumsum[np.arange(B), s.cutoff - 1].astype(np.float64)
+    zp64 = c64[np.arange(B), cut64 - 1]
+    assert (np.abs(zp32 - zp64)[agree] / zp64[agree]).max() < 1e-5
+
+
+def test_a_temperature_applied_the_wrong_way_would_fail_the_fp64_check():
+    # planted mistake: multiplying by T instead of dividing (the two agree only at T = 1)
+    x, u = _rows_case(seed=61, B=4)
+    s = O.sample(x, "bfloat16", 200, 0.95, u, return_stages=True,
+                 temperature=np.full(4, 0.5, np.float32))
+    p_wrong, _, _, _ = O.stages_f64(x, "bfloat16", 200, 0.95, temperature=2.0)
+    rel = np.abs(s.probs - p_wrong) / np.maximum(p_wrong, 1e-30)
+    assert rel[p_wrong > 1e-20].max() > 1e-2
+
+
 # --- a planted mistake is caught (the checks above are not vacuous) -----------------------------------
 
 def test_an_inclusive_prefix_cut_would_fail_the_closed_forms():
