@@ -32,20 +32,22 @@ constexpr int DPP_ROW_BCAST31 = 0x143;
 
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63); }
 
-// value of lane (l ^ J) for J in {1, 2, 4, 8, 16, 32}
+// value of lane (l ^ J) for J in {1, 2, 4, 8, 16, 32}.  The DPP moves leave no lane without
+// a source (quad permutes and row rotates), or only lanes whose result the select below
+// discards (row_shl:4 / row_shr:4), so they need no defined "old" value (mov_dpp).
 template <int J>
 __device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
   const int x = (int)v;
   if constexpr (J == 1) {
-    return (uint32_t)__builtin_amdgcn_update_dpp(0, x, DPP_QUAD_XOR1, 0xF, 0xF, false);
+    return (uint32_t)__builtin_amdgcn_mov_dpp(x, DPP_QUAD_XOR1, 0xF, 0xF, false);
   } else if constexpr (J == 2) {
-    return (uint32_t)__builtin_amdgcn_update_dpp(0, x, DPP_QUAD_XOR2, 0xF, 0xF, false);
+    return (uint32_t)__builtin_amdgcn_mov_dpp(x, DPP_QUAD_XOR2, 0xF, 0xF, false);
   } else if constexpr (J == 4) {
-    const int up = __builtin_amdgcn_update_dpp(0, x, DPP_ROW_SHL4, 0xF, 0xF, false);
-    const int dn = __builtin_amdgcn_update_dpp(0, x, DPP_ROW_SHR4, 0xF, 0xF, false);
+    const int up = __builtin_amdgcn_mov_dpp(x, DPP_ROW_SHL4, 0xF, 0xF, false);
+    const int dn = __builtin_amdgcn_mov_dpp(x, DPP_ROW_SHR4, 0xF, 0xF, false);
     return (uint32_t)((lane_id() & 4) ? dn : up);
   } else if constexpr (J == 8) {
-    return (uint32_t)__builtin_amdgcn_update_dpp(0, x, DPP_ROW_ROR8, 0xF, 0xF, false);
+    return (uint32_t)__builtin_amdgcn_mov_dpp(x, DPP_ROW_ROR8, 0xF, 0xF, false);
   } else if constexpr (J == 16) {
     // swap(v, v): result[0] (vdst) has the even 16-lane rows' values in the odd rows,
     // result[1] (vsrc) the odd rows' values in the even rows
@@ -68,17 +70,23 @@ __device__ __forceinline__ uint64_t xor_lane64(uint64_t v) {
 
 // One compare-exchange stage of a descending bitonic network over 64 lanes: block size K,
 // partner distance J.  Within a K-block the direction alternates so that the final K=64
-// merge leaves lane 0 with the largest value.
+// merge leaves lane 0 with the largest value.  A lane keeps the larger of (own, partner)
+// when it is the lower lane of a descending block or the upper lane of an ascending one.
+//   For 32-bit values max and min are single VALU ops and the lane-constant select follows
+// (no scalar step in the dependency chain); for 64-bit values one compare, xor-ed with the
+// lane-constant predicate, picks the partner or not.
 template <int K, int J, typename T>
 __device__ __forceinline__ T bitonic_step(T v) {
-  T o;
-  if constexpr (sizeof(T) == 8) o = (T)xor_lane64<J>((uint64_t)v);
-  else o = (T)xor_lane<J>((uint32_t)v);
   const int l = lane_id();
-  const bool desc = (l & K) == 0;
-  const bool lower = (l & J) == 0;
-  const T hi = v > o ? v : o, lo = v > o ? o : v;
-  return (lower == desc) ? hi : lo;
+  const bool keep_hi = ((l & J) == 0) == ((l & K) == 0);
+  if constexpr (sizeof(T) == 8) {
+    const T o = (T)xor_lane64<J>((uint64_t)v);
+    return ((o > v) == keep_hi) ? o : v;
+  } else {
+    const T o = (T)xor_lane<J>((uint32_t)v);
+    const T hi = v > o ? v : o, lo = v > o ? o : v;
+    return keep_hi ? hi : lo;
+  }
 }
 
 template <int K, int J, typename T>
@@ -172,10 +180,8 @@ __device__ __forceinline__ void net_stage(uint64_t (&v)[R]) {
     for (int i = 0; i < R; ++i) {
       const uint64_t o = xor_lane64<J / R>(v[i]);
       const int e = l * R + i;
-      const bool desc = ((e & K) == 0) != ASC;
-      const bool lower = (e & J) == 0;
-      const uint64_t hi = v[i] > o ? v[i] : o, lo = v[i] > o ? o : v[i];
-      v[i] = (lower == desc) ? hi : lo;
+      const bool keep_hi = ((e & J) == 0) == (((e & K) == 0) != ASC);
+      v[i] = ((o > v[i]) == keep_hi) ? o : v[i];
     }
   }
 }
@@ -196,6 +202,13 @@ __device__ __forceinline__ void net_sort_levels(uint64_t (&v)[R]) {
 template <int R>
 __device__ __forceinline__ void wave_sort_desc_n(uint64_t (&v)[R]) {
   net_sort_levels<R, 64 * R>(v);
+}
+
+// Full ascending sort of the 64*R words (every comparator mirrored): element 0 is the
+// smallest, which is the reversed layout wave_merge_top takes for its second list.
+template <int R>
+__device__ __forceinline__ void wave_sort_asc_n(uint64_t (&v)[R]) {
+  net_sort_levels<R, 64 * R, true>(v);
 }
 
 // v holds a descending list A; b_rev holds a descending list B with element e stored at
