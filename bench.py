@@ -251,6 +251,16 @@ def main() -> int:
     log(f"timing C5 cold: {args.warmup} warmup + {args.steps} steps")
     ms_cold = timed(c5_cold, args.steps, args.warmup)
     log(f"C5 cold {ms_cold * 1e3:.2f} us/call")
+    # the same cold calls issued from a HIP graph (one replay = one call on each buffer)
+    gi = [0]
+
+    def c5_cold_graphable():
+        i = gi[0]
+        gi[0] = i + 1
+        fused.sample_fused_u(bufs[i % ROTATE], 50, 0.90, u5)
+
+    ms_cold_graph = graph_per_call_ms(c5_cold_graphable, calls=ROTATE, replays=max(20, args.steps // ROTATE))
+    log(f"C5 cold from a HIP graph {ms_cold_graph * 1e3:.2f} us/call")
     ms_hot = median_of(c5_hot, max(200, args.steps // 4), 20, reps=3)
     log(f"C5 hot {ms_hot * 1e3:.2f} us/call")
     B5, V5 = c5.batch, c5.vocab
@@ -277,6 +287,26 @@ def main() -> int:
     plan1 = fused_sampling.make_plan(x1, 50)
     log(f"C1 {c1_us:.2f} us/call eager, {c1_graph_us:.2f} graph; floor {floor_us:.2f} / "
         f"{floor_graph_us:.2f}")
+
+    # the other BASELINE configs, eager back-to-back calls (hot: one buffer each)
+    others = {}
+    for name in ("C2_B1_k50", "C2_B64_k50", "C3", "C4_k256", "C4_k1024"):
+        c = W.case(name)
+        xc = to_dev(c.logits, c.dtype)
+        uc = torch.from_numpy(c.u).cuda()
+        gotc = fused.sample_fused_u(xc, c.top_k, c.top_p, uc).cpu().numpy()
+        if not np.array_equal(gotc, fix[f"{name}/token_ids"]):
+            print(f"{name} token ids differ from the golden fixture", file=sys.stderr)
+            return 1
+        call = lambda xc=xc, uc=uc, c=c: fused.sample_fused_u(xc, c.top_k, c.top_p, uc)  # noqa: E731
+        us = median_of(call, 1000, 50, reps=3) * 1e3
+        pl = fused_sampling.make_plan(xc, c.top_k)
+        others[name] = {"B": c.batch, "V": c.vocab, "k": c.top_k, "p": c.top_p,
+                        "us_per_call": round(us, 3),
+                        "gbps": round(algo_bytes(c.batch, c.vocab) / (us * 1e-6) / 1e9, 1),
+                        "plan": {"splits": pl.splits, "threads": pl.threads,
+                                 "chunks": pl.chunks}}
+        log(f"{name}: {us:.2f} us/call")
 
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "fsamp_kernel_c5_hbm_traffic.json")
@@ -315,6 +345,10 @@ def main() -> int:
         "cpu_baseline": cpu,
         "c5_hot": {"us_per_call": round(ms_hot * 1e3, 3), "gbps": round(gbps_hot, 1),
                    "note": "one buffer: served from the 256 MB MALL, not HBM"},
+        "c5_cold_graph": {"us_per_call": round(ms_cold_graph * 1e3, 3),
+                          "gbps": round(algo_bytes(B5, V5) / (ms_cold_graph * 1e-3) / 1e9, 1),
+                          "note": "the same cold calls replayed from a HIP graph"},
+        "configs": others,
         "c1": {"us_per_call": round(c1_us, 3), "us_per_call_graph": round(c1_graph_us, 3),
                "launches_per_call": 1, "launch_floor_us": round(floor_us, 3),
                "launch_floor_graph_us": round(floor_graph_us, 3),

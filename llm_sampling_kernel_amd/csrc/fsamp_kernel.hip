@@ -146,18 +146,22 @@ enum { M_HB = 0, M_ABOVE, M_LB, M_GT, M_CNT, M_RED };
 
 // ---- block primitives ----------------------------------------------------------------------
 
-// LDS atomics that many lanes aim at one address serialise.  Here each distinct bin among the
-// active lanes of the wave gets one atomicAdd carrying the lane count (the radix fallback runs
-// on tie-heavy data, where most lanes share a bin).
+// LDS atomics that many lanes aim at one address serialise.  The two most common bins of the
+// wave's active lanes (found by the first active lanes) get one atomic each carrying their
+// lane counts -- on tie-heavy data that is every lane -- and the lanes left over, whose bins
+// are spread, add 1 each to their own bin in parallel.
 __device__ __forceinline__ void wave_add(uint32_t* base, uint32_t bin, bool active) {
   uint64_t todo = __ballot(active);
-  while (todo != 0ull) {
+#pragma unroll
+  for (int round = 0; round < 2; ++round) {
+    if (todo == 0ull) return;
     const int leader = __builtin_ctzll(todo);
     const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)bin, leader);
-    const uint64_t same = __ballot(active && bin == b);
+    const uint64_t same = __ballot(active && bin == b) & todo;
     if (lane_id() == leader) atomicAdd(&base[b], (uint32_t)__popcll(same));
     todo &= ~same;
   }
+  if ((todo >> lane_id()) & 1ull) atomicAdd(&base[bin], 1u);
 }
 
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
@@ -249,22 +253,64 @@ __device__ __forceinline__ void zero_hist(uint32_t* hist) {
   for (int i = threadIdx.x; i < NSUB * 256; i += NT) hist[i] = 0u;
 }
 
-// Top-K of C unique words in cand[] (C <= NT), written to out[0..min(K, C)) in descending
-// order: each thread ranks one word by counting the words above it (LDS broadcast reads).
+// One compare-exchange stage (partner distance J) of a bitonic network over a 64-word segment
+// held one word per lane: lanes of a descending block (desc) keep the larger word in the
+// lower lane.  For block sizes K < 64 the direction comes from the lane index; K == 64 and
+// every larger block take the segment's direction, seg_desc.
+template <int K, int J>
+__device__ __forceinline__ uint64_t seg_step(uint64_t v, bool seg_desc) {
+  const int l = lane_id();
+  const bool desc = K < 64 ? ((l & K) == 0) : seg_desc;
+  const bool keep_hi = ((l & J) == 0) == desc;
+  const uint64_t o = xor_lane64<J>(v);
+  return ((o > v) == keep_hi) ? o : v;
+}
+
+template <int K, int J>
+__device__ __forceinline__ uint64_t seg_merge(uint64_t v, bool seg_desc) {
+  v = seg_step<K, J>(v, seg_desc);
+  if constexpr (J > 1) v = seg_merge<K, J / 2>(v, seg_desc);
+  return v;
+}
+
+template <int K>
+__device__ __forceinline__ uint64_t seg_levels(uint64_t v, bool seg_desc) {
+  if constexpr (K > 2) v = seg_levels<K / 2>(v, seg_desc);
+  return seg_merge<K, K / 2>(v, seg_desc);
+}
+
+// Descending bitonic sort of a[0..P) in LDS by the whole workgroup, P a power of two >= 64
+// (element e of a block of size k runs descending when (e & k) == 0).  Levels up to 64 and,
+// in every larger level, the stages of partner distance below 64 run in registers on 64-word
+// segments (one word per lane, DPP exchanges, no barrier); only the stages of distance >= 64
+// go through LDS, one compare-exchange per thread and pair and a barrier each.
 template <int NT>
-__device__ __forceinline__ void rank_sort_topk(const uint64_t* cand, int C, int K, uint64_t* out) {
-  const int i = threadIdx.x;
-  if (i < C) {
-    const uint64_t v = cand[i];
-    int r = 0;
-    int j = 0;
-#pragma unroll 2
-    for (; j + 8 <= C; j += 8) {
-#pragma unroll
-      for (int q = 0; q < 8; ++q) r += (int)(cand[j + q] > v);
+__device__ __forceinline__ void block_bitonic_sort_desc(uint64_t* a, int P) {
+  constexpr int W = NT / 64;
+  const int l = lane_id(), w = threadIdx.x >> 6;
+  const int nseg = P >> 6;
+  for (int sg = w; sg < nseg; sg += W) {
+    const uint64_t v = a[sg * 64 + l];
+    a[sg * 64 + l] = seg_levels<64>(v, (sg & 1) == 0);
+  }
+  __syncthreads();
+  for (int k = 128; k <= P; k <<= 1) {
+    for (int j = k >> 1; j >= 64; j >>= 1) {
+      for (int i = threadIdx.x; i < (P >> 1); i += NT) {
+        const int e = ((i & ~(j - 1)) << 1) | (i & (j - 1));  // lower element of pair i
+        const uint64_t x = a[e], y = a[e + j];
+        if ((x < y) == ((e & k) == 0)) {
+          a[e] = y;
+          a[e + j] = x;
+        }
+      }
+      __syncthreads();
     }
-    for (; j < C; ++j) r += (int)(cand[j] > v);
-    if (r < K) out[r] = v;
+    for (int sg = w; sg < nseg; sg += W) {
+      const uint64_t v = a[sg * 64 + l];
+      a[sg * 64 + l] = seg_merge<64, 32>(v, ((sg * 64) & k) == 0);
+    }
+    __syncthreads();
   }
 }
 
@@ -319,6 +365,25 @@ __device__ __forceinline__ uint32_t wave_kth_u32(const uint32_t* src, int n, int
   for (int i = 0; i < R; ++i)
     if (l * R + i == e) mine = (uint32_t)v[i];
   return read_lane_u32(mine, e / R);
+}
+
+// Wave 0: copy the n words the row's workgroups handed over (agent-scope loads, which read
+// past the per-XCD L2) into LDS, eight loads in flight per lane before the first store.
+__device__ __forceinline__ void load_lists(const uint64_t* src, int n, uint64_t* dst) {
+  const int l = lane_id();
+  for (int i0 = 0; i0 < n; i0 += 8 * 64) {
+    uint64_t w[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int i = i0 + q * 64 + l;
+      w[q] = i < n ? __hip_atomic_load(&src[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int i = i0 + q * 64 + l;
+      if (i < n) dst[i] = w[q];
+    }
+  }
 }
 
 // Wave 0: merge S descending lists of K words (lists[s*K + i] in LDS, padded with zeros to
@@ -698,8 +763,7 @@ __device__ __forceinline__ void wave_tail_regs(const Params& p, Smem<NT>& sm, ui
     //    once), then fold them in registers
     const int n = p.S * p.K;
     const uint64_t* src = p.partials + (size_t)row * p.S * p.K;
-    for (int i = l; i < n; i += 64)
-      sm.g.cand[i] = __hip_atomic_load(&src[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    load_lists(src, n, sm.g.cand);
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     FSAMP_TRACE(7);
     wave_merge_lists<RB>(sm.g.cand, p.S, p.K, v);
@@ -756,8 +820,7 @@ __device__ __forceinline__ void wave_back_wide(const Params& p, Smem<NT>& sm, in
     }
     const int n = p.S * p.K;
     const uint64_t* src = p.partials + (size_t)row * p.S * p.K;
-    for (int i = l; i < n; i += 64)
-      sm.g.cand[i] = __hip_atomic_load(&src[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    load_lists(src, n, sm.g.cand);
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     FSAMP_TRACE(7);
     wave_merge_lists_dst<RB>(sm.g.cand, p.S, p.K, sm.top);
@@ -1071,12 +1134,22 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
     }
 
     // 4. the slice's top-keff, sorted: up to WSORT_MAX candidates go straight to wave 0's
-    //    register sort below; beyond that (heavy ties) an exact radix select over the
-    //    registers first reduces them to exactly keff.
+    //    register sort below; up to K_MAX (all of them in top[]) the workgroup sorts them in
+    //    LDS; beyond that an exact radix select over the registers first reduces them to
+    //    exactly keff.
     ncand = total;
-    if (total > WSORT_MAX || wave_over) {
-      // heavy ties: exact radix select over the registers -- threshold T, keys > T, and the
-      // lowest-id keys == T in id order -- into cand[0..keff), then rank them
+    if (total > WSORT_MAX && total <= FSAMP_K_MAX && !wave_over) {
+      // more candidates than wave 0 sorts in registers (heavy ties, wide k), but every one of
+      // them was gathered into top[]: the workgroup sorts them where they are
+      int P = 1;
+      while (P < total) P <<= 1;
+      for (int i = total + t; i < P; i += NT) sm.top[i] = 0ull;
+      __syncthreads();
+      block_bitonic_sort_desc<NT>(sm.top, P);
+      sorted_in_lds = true;
+    } else if (total > WSORT_MAX || wave_over) {
+      // candidates past the top[] buffer: exact radix select over the registers -- threshold
+      // T, keys > T, and the lowest-id keys == T in id order -- into cand[0..keff), then sort
       pass_barrier<CH>(kv);
       const int sub = wid & (NSUB - 1);
       zero_hist<NT>(sm.u.rx.hist);
@@ -1167,7 +1240,13 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
       ncand = keff;
       regions = false;
       if (keff > WSORT_MAX) {
-        rank_sort_topk<NT>(sm.g.cand, keff, keff, sm.top);
+        // exactly keff (<= K_MAX) words in cand[]: pad to a power of two and sort in place
+        int P = 1;
+        while (P < keff) P <<= 1;
+        for (int i = keff + t; i < P; i += NT) sm.g.cand[i] = 0ull;
+        __syncthreads();
+        block_bitonic_sort_desc<NT>(sm.g.cand, P);
+        for (int i = t; i < keff; i += NT) sm.top[i] = sm.g.cand[i];
         sorted_in_lds = true;
       }
       __syncthreads();
