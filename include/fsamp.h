@@ -197,8 +197,10 @@ int fsamp_debug_wave_selftest(uint32_t* out, hipStream_t stream);
 
 /* Tuning aid with no counterpart in the reference: fsamp_sample (explicit u) that also records
  * the shader clock (s_memtime) at fixed points of every workgroup into trace[workgroup*32 + i],
- * i < 16, and the constant 100 MHz clock (s_memrealtime) at its start and at the end of the
- * sampling tail into slots 16 and 17 (device, B*splits*32 int64, pre-filled by the caller). */
+ * i < 16, the constant 100 MHz clock (s_memrealtime) at its start and at the end of the
+ * sampling tail into slots 16 and 17, and the shader clock at which wave w (w < 14) has its
+ * whole share of the slice into slot 18 + w (device, B*splits*32 int64, pre-filled by the
+ * caller). */
 int fsamp_debug_sample_traced(const void* logits, int dtype, int64_t B, int64_t V,
                               int64_t top_k, double top_p, const float* u, int64_t* out,
                               void* ws, size_t ws_bytes, int64_t splits_override,

@@ -645,12 +645,36 @@ __device__ __forceinline__ uint32_t key_at(const uint32_t (&k)[4], int j) {
   return (j & 1) ? (w >> 16) : (w & 0xFFFFu);
 }
 
+// element j (0..15) of a chunk pair given as its eight words, j runtime: a select tree on the
+// bits of j / 2, then the half (values, so the select never becomes an address into kv[])
+__device__ __forceinline__ uint32_t key_of16(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3,
+                                             uint32_t w4, uint32_t w5, uint32_t w6, uint32_t w7,
+                                             int j) {
+  const int q = j >> 1;
+  const bool b0 = (q & 1) != 0, b1 = (q & 2) != 0, b2 = (q & 4) != 0;
+  const uint32_t x01 = b0 ? w1 : w0, x23 = b0 ? w3 : w2, x45 = b0 ? w5 : w4, x67 = b0 ? w7 : w6;
+  const uint32_t y0 = b1 ? x23 : x01, y1 = b1 ? x67 : x45;
+  const uint32_t w = b2 ? y1 : y0;
+  return (j & 1) ? (w >> 16) : (w & 0xFFFFu);
+}
+
 // Phase timestamps for tuning: thread 0 of each workgroup records the shader clock at fixed
 // points into trace[workgroup * 16 + i] when the caller passes a trace buffer.
 #define FSAMP_TRACE(i)                                                                       \
   do {                                                                                       \
     if (p.trace != nullptr && threadIdx.x == 0)                                              \
       p.trace[(size_t)blockIdx.x * 32 + (i)] = (int64_t)__builtin_amdgcn_s_memtime();        \
+  } while (0)
+// lane 0 of wave w (w < 14) records the shader clock at which the wave has all of its loads
+// into slot 18 + w (the wait is explicit: the compiler would otherwise hoist the clock read
+// above the code that consumes the loads)
+#define FSAMP_WTRACE()                                                                       \
+  do {                                                                                       \
+    if (p.trace != nullptr && lane_id() == 0 && (threadIdx.x >> 6) < 14) {                   \
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");                                       \
+      p.trace[(size_t)blockIdx.x * 32 + 18 + (threadIdx.x >> 6)] =                           \
+          (int64_t)__builtin_amdgcn_s_memtime();                                             \
+    }                                                                                        \
   } while (0)
 // the constant-rate (100 MHz) clock into slot 16 + i, to convert shader clocks to time
 #define FSAMP_RTRACE(i)                                                                      \
@@ -674,9 +698,27 @@ template <int RB, int NT>
 __device__ __forceinline__ void wave_tail_regs(const Params& p, Smem<NT>& sm, uint64_t (&v)[RB],
                                                int keff, int row, int split, const RowCtl& rc);
 
+// Sorts up to 64 candidate words >= L descending, one per lane.  When every candidate key
+// lies in [L, L + 2^14) (L >= 0xC000: the slice's bound sits in the top quarter of the key
+// range, as for any row whose top values are positive) and ids fit in 18 bits, each word is
+// (key - L) << 18 | (2^18 - 1 - id): the same order in 32 bits, which halves the network's
+// work.  Zero words (padding) stay zero and sort last either way.
+__device__ __forceinline__ uint64_t wave_sort64_words(uint64_t v, uint32_t L, int V) {
+  if (L >= 0xC000u && V < (1 << 18)) {
+    uint32_t w = 0u;
+    if (v != 0ull) w = (((uint32_t)(v >> 32) - L) << 18) | ((uint32_t)(0x3FFFF - unpack_id(v)));
+    w = wave_sort_desc<uint32_t>(w);
+    return w != 0u ? pack((w >> 18) + L, 0x3FFFFu - (w & 0x3FFFFu)) : 0ull;
+  }
+  uint64_t a[1] = {v};
+  wave_sort_desc_n<1>(a);
+  return a[0];
+}
+
 template <int RB, int NT>
 __device__ __forceinline__ void wave_back(const Params& p, Smem<NT>& sm, int keff, int ncand, bool sorted_in_lds,
-                          bool regions, int row, int split, const RowCtl& rc) {
+                          bool regions, int row, int split, const RowCtl& rc, uint32_t L,
+                          uint64_t pre) {
   if constexpr (RB > 4) {
     wave_back_wide<RB, NT>(p, sm, keff, ncand, sorted_in_lds, regions, row, split, rc);
     return;
@@ -687,7 +729,12 @@ __device__ __forceinline__ void wave_back(const Params& p, Smem<NT>& sm, int kef
     // candidates are contiguous: in top[] from the gather, in cand[] from the radix select
     const uint64_t* base = regions ? sm.top : sm.g.cand;
     auto load = [&](int e) -> uint64_t { return base[e]; };
-    if (ncand <= 64 * RB) {
+    if (RB == 1 && regions && ncand <= 64) {
+      // top[0..64) was read right after the gather barrier (zero past the candidates)
+      FSAMP_TRACE(14);
+      v[0] = wave_sort64_words(pre, L, p.V);
+      if (l >= keff) v[0] = 0ull;
+    } else if (ncand <= 64 * RB) {
 #pragma unroll
       for (int i = 0; i < RB; ++i) {
         const int e = l * RB + i;
@@ -851,11 +898,31 @@ __device__ __forceinline__ uint32_t opaque_base(int lo, int t) {
   return b;
 }
 
+// Zero words that absent per-row inputs are read from instead (never written).
+__device__ uint64_t g_zero_words[2];
+
+// 0 in a VGPR, opaque to the optimiser (a per-lane value as far as it can tell)
+__device__ __forceinline__ int opaque_vzero() {
+  int z;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+  return z;
+}
+
 // compile-time integer for the pair ranges of the gather
 template <int N>
 struct IC {
   static constexpr int value = N;
 };
+
+// f(IC<I>{}) for I = I0 .. I1-1 in order: loop bodies whose register indexes must be
+// compile-time constants, however large the unrolled body grows
+template <int I0, int I1, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I0 < I1) {
+    f(IC<I0>{});
+    static_for<I0 + 1, I1>(f);
+  }
+}
 
 template <int NT, int CH, bool VEC>
 __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
@@ -874,32 +941,54 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
   const int keff = min(p.K, count);
   FSAMP_TRACE(0);
   FSAMP_RTRACE(0);
-  // the row's uniform and controls, fetched now so that their latency hides under the loads
-  RowCtl rc;
-  if (p.u != nullptr) {
-    rc.u = p.u[row];
-  } else {
-    const uint64_t off = p.offset_ctr != nullptr
-                             ? __hip_atomic_load(p.offset_ctr, __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT)
-                             : p.offset;
-    rc.u = rng_uniform(p.seed, off, (uint32_t)row);
-  }
-  rc.k = p.K;
-  rc.top_p = p.top_p_f;
-  rc.keep_all = p.keep_all;
-  rc.inv_t = 1.0f;
-  if (p.topk_row != nullptr) rc.k = min(max(p.topk_row[row], 1), p.K);
-  if (p.topp_row != nullptr) {
-    rc.top_p = p.topp_row[row];
-    rc.keep_all = rc.top_p >= 1.0f ? 1 : 0;
-  }
-  if (p.temp_row != nullptr) {
-    const float T = p.temp_row[row];
-    if (T > 0.0f) rc.inv_t = 1.0f / T;
-    else rc.k = 1;  // temperature <= 0 (or NaN): greedy
-  }
+  // The row's uniform, offset and controls are fetched now, so that their latency hides under
+  // the slice loads, and only read at the tail (row_ctl): a value consumed here would make the
+  // wave wait for its load before issuing the slice loads.  Every one is loaded
+  // unconditionally, an absent one from a zero word, so that no branch joins registers with
+  // loads pending on one side (which also makes the wave wait), and the index carries a zero
+  // the compiler cannot see through, so that the values stay in VGPRs (a load from a uniform
+  // address would be moved to SGPRs right where it is issued, which waits for it).
+  const int vz = opaque_vzero();
+  const uint64_t* zw = g_zero_words;
+  const float u_ld = (p.u != nullptr ? p.u + row : reinterpret_cast<const float*>(zw))[vz];
+  const uint64_t off_ld = __hip_atomic_load((p.offset_ctr != nullptr ? p.offset_ctr : zw) + vz,
+                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const int32_t topk_ld =
+      (p.topk_row != nullptr ? p.topk_row + row : reinterpret_cast<const int32_t*>(zw))[vz];
+  const float topp_ld =
+      (p.topp_row != nullptr ? p.topp_row + row : reinterpret_cast<const float*>(zw))[vz];
+  const float temp_ld =
+      (p.temp_row != nullptr ? p.temp_row + row : reinterpret_cast<const float*>(zw))[vz];
+  auto row_ctl = [&]() -> RowCtl {
+    // (made opaque here, so that no arithmetic on them is hoisted next to their loads)
+    float u_v = u_ld, topp_v = topp_ld, temp_v = temp_ld;
+    int32_t topk_v = topk_ld;
+    uint64_t off_v = off_ld;
+    asm volatile("" : "+v"(u_v), "+v"(topp_v), "+v"(temp_v), "+v"(topk_v), "+v"(off_v));
+    RowCtl rc;
+    if (p.u != nullptr) {
+      rc.u = u_v;
+    } else {
+      const uint64_t off = p.offset_ctr != nullptr ? off_v : p.offset;
+      rc.u = rng_uniform(p.seed, off, (uint32_t)row);
+    }
+    rc.k = p.K;
+    rc.top_p = p.top_p_f;
+    rc.keep_all = p.keep_all;
+    rc.inv_t = 1.0f;
+    if (p.topk_row != nullptr) rc.k = min(max(topk_v, 1), p.K);
+    if (p.topp_row != nullptr) {
+      rc.top_p = topp_v;
+      rc.keep_all = rc.top_p >= 1.0f ? 1 : 0;
+    }
+    if (p.temp_row != nullptr) {
+      if (temp_v > 0.0f) rc.inv_t = 1.0f / temp_v;
+      else rc.k = 1;  // temperature <= 0 (or NaN): greedy
+    }
+    return rc;
+  };
   if (t == 0) sm.misc[M_CNT] = 0;
+  if (t < 64) sm.top[t] = 0ull;  // the first 64 candidate slots, read whole after the gather
 
   // 1. load the slice into registers as packed keys (padding = key 0).  With VEC, V and the
   //    split bounds are multiples of 8, so a chunk is all in or all out; chunks past the slice
@@ -1021,16 +1110,19 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
 #pragma unroll
     for (int i = I0; i < I1; ++i) {
       const bool hit = pkmax(pm[i], lm1) != lm1;
-      if (hit && nst < STAGE_SLOTS) {
-        sm.g.st.a[nst][t] = make_uint4(kv[2 * i][0], kv[2 * i][1], kv[2 * i][2], kv[2 * i][3]);
-        if (2 * i + 1 < CH)
-          sm.g.st.b[nst][t] = make_uint4(kv[2 * i + 1][0], kv[2 * i + 1][1], kv[2 * i + 1][2],
-                                         kv[2 * i + 1][3]);
-        else
-          sm.g.st.b[nst][t] = make_uint4(0u, 0u, 0u, 0u);
-        sm.meta[nst][t] = (uint8_t)i;
+      // most pairs hold no qualifying lane in the whole wave: one scalar branch skips them
+      if (__ballot(hit) != 0ull) {
+        if (hit && nst < STAGE_SLOTS) {
+          sm.g.st.a[nst][t] = make_uint4(kv[2 * i][0], kv[2 * i][1], kv[2 * i][2], kv[2 * i][3]);
+          if (2 * i + 1 < CH)
+            sm.g.st.b[nst][t] = make_uint4(kv[2 * i + 1][0], kv[2 * i + 1][1], kv[2 * i + 1][2],
+                                           kv[2 * i + 1][3]);
+          else
+            sm.g.st.b[nst][t] = make_uint4(0u, 0u, 0u, 0u);
+          sm.meta[nst][t] = (uint8_t)i;
+        }
+        nst += hit ? 1 : 0;
       }
-      nst += hit ? 1 : 0;
     }
   };
   auto extract = [&](uint32_t L, int nst, uint64_t* region_base, int rw, int32_t* wc) {
@@ -1096,7 +1188,7 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
 
 #pragma unroll
   for (int c = 0; c < CH; ++c) convert(c);
-  FSAMP_TRACE(1);
+  FSAMP_WTRACE();
   const uint32_t tmax = tmax_of(IC<0>{}, IC<NP>{});
 
   if (p.stop == 1) {
@@ -1112,6 +1204,8 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
   // Single-phase selection: L from every thread maximum, one gather, and the exact radix
   // select when the candidates overflow.
   int ncand = 0;
+  uint64_t pre = 0ull;
+  uint32_t L_sel = 1u;
   bool sorted_in_lds = false;
   bool regions = true;  // candidates in per-wave regions of top[] (else contiguous in cand[])
   if (keff > 0) {
@@ -1124,6 +1218,8 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
     stage(IC<0>{}, IC<NP>{}, L, nst);
     extract(L, nst, sm.top, FSAMP_K_MAX, &sm.misc[M_CNT]);
     __syncthreads();
+    pre = sm.top[lane];  // issued with the count read below: one LDS round trip for both
+    L_sel = L;
     FSAMP_TRACE(4);
     // LDS loads count as divergent to the compiler; the total is uniform by construction
     const int total = __builtin_amdgcn_readfirstlane(sm.misc[M_CNT]);
@@ -1197,6 +1293,7 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
       __syncthreads();
       find_bucket<NT>(sm.u.rx.suf, keff - above, above, &sm.misc[M_LB], &sm.misc[M_GT]);
       if (t == 0) sm.misc[M_CNT] = 0;
+  if (t < 64) sm.top[t] = 0ull;  // the first 64 candidate slots, read whole after the gather
       __syncthreads();
       const uint32_t T = (hb << 8) | (uint32_t)sm.misc[M_LB];
       const int n_gt = sm.misc[M_GT];
@@ -1255,11 +1352,16 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
 
   // From here on wave 0 carries the workgroup alone: no more workgroup barriers.
   if (wid != 0) return;
-  if (p.K <= 64) wave_back<1, NT>(p, sm, keff, ncand, sorted_in_lds, regions, row, split, rc);
-  else if (p.K <= 128) wave_back<2, NT>(p, sm, keff, ncand, sorted_in_lds, regions, row, split, rc);
-  else if (p.K <= 256) wave_back<4, NT>(p, sm, keff, ncand, sorted_in_lds, regions, row, split, rc);
-  else if (p.K <= 512) wave_back<8, NT>(p, sm, keff, ncand, sorted_in_lds, regions, row, split, rc);
-  else wave_back<16, NT>(p, sm, keff, ncand, sorted_in_lds, regions, row, split, rc);
+  const RowCtl rc = row_ctl();
+  auto back = [&](auto rbc) {
+    constexpr int RB = decltype(rbc)::value;
+    wave_back<RB, NT>(p, sm, keff, ncand, sorted_in_lds, regions, row, split, rc, L_sel, pre);
+  };
+  if (p.K <= 64) back(IC<1>{});
+  else if (p.K <= 128) back(IC<2>{});
+  else if (p.K <= 256) back(IC<4>{});
+  else if (p.K <= 512) back(IC<8>{});
+  else back(IC<16>{});
 }
 
 // ---- instantiation table -----------------------------------------------------------------------
