@@ -665,13 +665,13 @@ __device__ __forceinline__ uint32_t key_of16(uint32_t w0, uint32_t w1, uint32_t 
     if (p.trace != nullptr && threadIdx.x == 0)                                              \
       p.trace[(size_t)blockIdx.x * 32 + (i)] = (int64_t)__builtin_amdgcn_s_memtime();        \
   } while (0)
-// lane 0 of wave w (w < 14) records the shader clock at which the wave has all of its loads
-// into slot 18 + w (the wait is explicit: the compiler would otherwise hoist the clock read
-// above the code that consumes the loads)
-#define FSAMP_WTRACE()                                                                       \
+// lane 0 of wave w (w < 14) records the shader clock once `dep` (a value computed from all
+// of the wave's loads) exists into slot 18 + w; the empty asm consuming it keeps the clock
+// read from being hoisted above that computation
+#define FSAMP_WTRACE(dep)                                                                    \
   do {                                                                                       \
     if (p.trace != nullptr && lane_id() == 0 && (threadIdx.x >> 6) < 14) {                   \
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");                                       \
+      asm volatile("" ::"v"(dep));                                                           \
       p.trace[(size_t)blockIdx.x * 32 + 18 + (threadIdx.x >> 6)] =                           \
           (int64_t)__builtin_amdgcn_s_memtime();                                             \
     }                                                                                        \
@@ -730,9 +730,9 @@ __device__ __forceinline__ void wave_back(const Params& p, Smem<NT>& sm, int kef
     const uint64_t* base = regions ? sm.top : sm.g.cand;
     auto load = [&](int e) -> uint64_t { return base[e]; };
     if (RB == 1 && regions && ncand <= 64) {
-      // top[0..64) was read right after the gather barrier (zero past the candidates)
+      // top[0..64) was read right after the gather barrier
       FSAMP_TRACE(14);
-      v[0] = wave_sort64_words(pre, L, p.V);
+      v[0] = wave_sort64_words(l < ncand ? pre : 0ull, L, p.V);
       if (l >= keff) v[0] = 0ull;
     } else if (ncand <= 64 * RB) {
 #pragma unroll
@@ -1188,8 +1188,8 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
 
 #pragma unroll
   for (int c = 0; c < CH; ++c) convert(c);
-  FSAMP_WTRACE();
   const uint32_t tmax = tmax_of(IC<0>{}, IC<NP>{});
+  FSAMP_WTRACE(tmax);
 
   if (p.stop == 1) {
     const uint32_t wmax = wave_max_u32(tmax);
@@ -1293,7 +1293,6 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
       __syncthreads();
       find_bucket<NT>(sm.u.rx.suf, keff - above, above, &sm.misc[M_LB], &sm.misc[M_GT]);
       if (t == 0) sm.misc[M_CNT] = 0;
-  if (t < 64) sm.top[t] = 0ull;  // the first 64 candidate slots, read whole after the gather
       __syncthreads();
       const uint32_t T = (hb << 8) | (uint32_t)sm.misc[M_LB];
       const int n_gt = sm.misc[M_GT];
