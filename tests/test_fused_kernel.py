@@ -156,6 +156,37 @@ def test_tie_grid_rows_through_every_path():
         assert np.array_equal(fused.topk_fused(x, 50, splits=s).cpu().numpy(), want), s
 
 
+@pytest.mark.parametrize("shift, scale", [(-20.0, 1.0), (1.0, 0.25), (0.0, 3.0)])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_candidate_sort_matches_the_oracle_on_either_side_of_its_32_bit_form(shift, scale, dtype):
+    # up to 64 candidates are sorted as 32-bit words when the bound's key is >= 0xC000 (rows
+    # whose top values are at least 2.0); all-negative rows and rows of small values take the
+    # 64-bit words instead.  Both must give the oracle's candidates, order and tokens.
+    x32 = np.random.Generator(np.random.PCG64(91)).standard_normal((6, 50000)).astype(np.float32)
+    bits = W.to_bits(x32 * scale + shift, dtype)
+    x = dev(bits, dtype)
+    u = ustream(6, 92)
+    want = oracle(bits, dtype, 50, 0.9, u)
+    tok, _, keep, ren = run_u(x, 50, 0.9, u)
+    assert np.array_equal(fused_sampling.topk_fused(x, 50, 0).cpu().numpy(), want.topk_ids)
+    assert np.array_equal(tok, want.token_ids)
+    assert np.array_equal(ren.view(np.uint32), want.renormed.view(np.uint32))
+
+
+def test_vocabularies_past_18_bit_ids_keep_the_exact_order():
+    # ids of 2^18 and more do not fit the 32-bit sort words: those slices sort 64-bit words
+    V = (1 << 18) + 4000
+    bits = randn_bits((3, V), 93, 3.0, "bfloat16")
+    x = dev(bits, "bfloat16")
+    u = ustream(3, 94)
+    want = oracle(bits, "bfloat16", 50, 0.9, u)
+    for s in (0, 1):
+        tok, _, keep, ren = run_u(x, 50, 0.9, u, s)
+        assert np.array_equal(fused_sampling.topk_fused(x, 50, s).cpu().numpy(), want.topk_ids), s
+        assert np.array_equal(tok, want.token_ids), s
+        assert np.array_equal(ren.view(np.uint32), want.renormed.view(np.uint32)), s
+
+
 def test_every_split_count_and_workgroup_size_gives_the_same_answer():
     bits = randn_bits((4, 151936), 45, 3.0, "bfloat16")
     x = dev(bits, "bfloat16")
