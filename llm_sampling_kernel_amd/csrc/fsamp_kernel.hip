@@ -81,8 +81,10 @@ __device__ __forceinline__ uint32_t unpack_id(uint64_t w) {
 // key -> fp32 value (the exact bf16/fp16 value; the -0 key decodes to +0)
 __device__ __forceinline__ float key_to_float(uint32_t key, int is_bf16) {
   const uint32_t b = (key & 0x8000u) ? (key & 0x7FFFu) : ((0x10000u - key) & 0xFFFFu);
-  if (is_bf16) return __uint_as_float(b << 16);
-  return (float)__builtin_bit_cast(_Float16, (unsigned short)b);
+  // both decodes and a select: no branch in the latency-bound tail
+  const float as_bf16 = __uint_as_float(b << 16);
+  const float as_f16 = (float)__builtin_bit_cast(_Float16, (unsigned short)b);
+  return is_bf16 ? as_bf16 : as_f16;
 }
 
 // ---- fp32 tail helpers -------------------------------------------------------------------
@@ -91,7 +93,10 @@ __device__ __forceinline__ float key_to_float(uint32_t key, int is_bf16) {
 // |r| <= ln2/2 by Horner with fma, scale by 2^n from exponent bits; x < -86 gives 0.
 // Bit-identical to the CPU oracle's exp, which evaluates the same operations in the same order.
 __device__ __forceinline__ float exp_nonpos(float x) {
-  if (!(x >= -86.0f)) return 0.0f;
+  // evaluated for every x and selected at the end (no branch); below -86, or for NaN, the
+  // intermediate scale is meaningless and the select returns 0
+  const bool in_range = x >= -86.0f;
+  x = in_range ? x : 0.0f;
   const float n = rintf(x * 1.44269504088896341f);
   float r = __builtin_fmaf(-n, 0.693145751953125f, x);
   r = __builtin_fmaf(-n, 1.42860682030941723e-6f, r);
@@ -104,7 +109,8 @@ __device__ __forceinline__ float exp_nonpos(float x) {
   p = __builtin_fmaf(p, r, 1.0f);
   p = __builtin_fmaf(p, r, 1.0f);
   const int ni = (int)n;
-  return p * __uint_as_float((uint32_t)(ni + 127) << 23);
+  const float e = p * __uint_as_float((uint32_t)(ni + 127) << 23);
+  return in_range ? e : 0.0f;
 }
 
 // splitmix64 finalizer over (seed, offset, row): 24-bit uniform in [0, 1)
@@ -484,37 +490,34 @@ __device__ __forceinline__ void sample_tail(const Params& p, const uint64_t (&v)
   float w[RB], pr[RB], c[RB];
   const float m = FROM_LDS ? key_to_float((uint32_t)(top[0] >> 32), p.is_bf16)
                            : key_to_float(read_lane_u32((uint32_t)(v[0] >> 32), 0), p.is_bf16);
+  // ranks past K (or past R per lane) carry w = p = 0: adding +0 to the non-negative sums
+  // leaves them bit-identical, so the guards are selects and the tail runs without branches
   float s = 0.0f;
 #pragma unroll
   for (int j = 0; j < RB; ++j) {
-    w[j] = 0.0f;
-    if (j < R && base + j < K) {
-      const float x = key_to_float((uint32_t)(word(j) >> 32), p.is_bf16);
-      w[j] = exp_nonpos((x - m) * rc.inv_t);
-      s = s + w[j];
-    }
+    const bool valid = j < R && base + j < K;
+    const float x = key_to_float((uint32_t)(word(j) >> 32), p.is_bf16);
+    const float e = exp_nonpos((x - m) * rc.inv_t);
+    w[j] = valid ? e : 0.0f;
+    s = s + w[j];
   }
   const float z = read_lane_f32(wave_incl_scan_f32(s), 63);
   float tsum = 0.0f;
 #pragma unroll
   for (int j = 0; j < RB; ++j) {
-    pr[j] = 0.0f;
-    if (j < R && base + j < K) {
-      pr[j] = w[j] / z;
-      tsum = tsum + pr[j];
-    }
+    pr[j] = w[j] / z;
+    tsum = tsum + pr[j];
   }
   float acc = wave_shr1_f32(wave_incl_scan_f32(tsum));
   int my_drop = K;
 #pragma unroll
   for (int j = 0; j < RB; ++j) {
-    c[j] = 0.0f;
-    if (j < R && base + j < K) {
-      acc = acc + pr[j];
-      c[j] = acc;
-      const int idx = base + j;
-      if (idx >= 1 && my_drop == K && !((c[j] - pr[j]) < rc.top_p)) my_drop = idx;
-    }
+    const int idx = base + j;
+    const bool valid = j < R && idx < K;
+    acc = acc + pr[j];  // + 0 past the valid ranks
+    c[j] = valid ? acc : 0.0f;
+    const bool drop = valid && idx >= 1 && my_drop == K && !((c[j] - pr[j]) < rc.top_p);
+    my_drop = drop ? idx : my_drop;
   }
   // lanes hold consecutive rank ranges, so the lowest lane with a hit has the first hit
   const uint64_t drops = __ballot(my_drop < K);
@@ -530,7 +533,8 @@ __device__ __forceinline__ void sample_tail(const Params& p, const uint64_t (&v)
 #pragma unroll
   for (int j = 0; j < RB; ++j) {
     const int idx = base + j;
-    if (j < R && idx <= r && my_pick == K && c[j] >= target) my_pick = idx;
+    const bool pick = j < R && idx <= r && my_pick == K && c[j] >= target;
+    my_pick = pick ? idx : my_pick;
   }
   const uint64_t hits = __ballot(my_pick < K);
   const int pick = hits ? __builtin_amdgcn_readlane(my_pick, __builtin_ctzll(hits)) : r;
