@@ -320,6 +320,31 @@ __device__ __forceinline__ void block_bitonic_sort_desc(uint64_t* a, int P) {
   }
 }
 
+// The descending top 64 of a[0..P) into a[0..64), P a power of two >= 128, by the whole
+// workgroup: every 64-word segment is sorted in registers by one wave (DPP network), then
+// pairs of sorted segments are folded by bitonic top-merges (elementwise maximum of one list
+// and the other reversed, then half-cleaners) in log2(P/64) rounds, each round's merges
+// running in parallel across the waves with a barrier between rounds.  For k <= 64 this
+// does a fraction of the full sort's work (no LDS stages of partner distance >= 64).
+template <int NT>
+__device__ __forceinline__ void block_top64_desc(uint64_t* a, int P) {
+  constexpr int W = NT / 64;
+  const int l = lane_id(), w = threadIdx.x >> 6;
+  const int nseg = P >> 6;
+  for (int sg = w; sg < nseg; sg += W) a[sg * 64 + l] = wave_sort_desc<uint64_t>(a[sg * 64 + l]);
+  __syncthreads();
+  for (int step = 1; step < nseg; step <<= 1) {
+    for (int m = w; m < (nseg >> 1) / step; m += W) {
+      const int lo = m * 2 * step, hi = lo + step;
+      uint64_t v[1] = {a[lo * 64 + l]};
+      const uint64_t b_rev[1] = {a[hi * 64 + 63 - l]};
+      wave_merge_top<1>(v, b_rev);
+      a[lo * 64 + l] = v[0];
+    }
+    __syncthreads();
+  }
+}
+
 // ---- wave-0 selection helpers ------------------------------------------------------------------
 
 constexpr int WSORT_MAX = 256;  // candidates wave 0 sorts in registers (4 words per lane)
@@ -1245,7 +1270,8 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
       while (P < total) P <<= 1;
       for (int i = total + t; i < P; i += NT) sm.top[i] = 0ull;
       __syncthreads();
-      block_bitonic_sort_desc<NT>(sm.top, P);
+      if (keff <= 64) block_top64_desc<NT>(sm.top, P);
+      else block_bitonic_sort_desc<NT>(sm.top, P);
       sorted_in_lds = true;
     } else if (total > WSORT_MAX || wave_over) {
       // candidates past the top[] buffer: exact radix select over the registers -- threshold
