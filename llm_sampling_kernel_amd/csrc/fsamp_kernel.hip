@@ -320,26 +320,39 @@ __device__ __forceinline__ void block_bitonic_sort_desc(uint64_t* a, int P) {
   }
 }
 
-// The descending top 64 of a[0..P) into a[0..64), P a power of two >= 128, by the whole
-// workgroup: every 64-word segment is sorted in registers by one wave (DPP network), then
-// pairs of sorted segments are folded by bitonic top-merges (elementwise maximum of one list
-// and the other reversed, then half-cleaners) in log2(P/64) rounds, each round's merges
-// running in parallel across the waves with a barrier between rounds.  For k <= 64 this
-// does a fraction of the full sort's work (no LDS stages of partner distance >= 64).
-template <int NT>
-__device__ __forceinline__ void block_top64_desc(uint64_t* a, int P) {
+// The descending top 64R of a[0..P) into a[0..64R), P a power of two >= 128R, by the whole
+// workgroup: every 64R-word segment is sorted in registers by one wave (DPP network, element
+// l*R + i in lane l), then pairs of sorted segments are folded by bitonic top-merges
+// (elementwise maximum of one list and the other reversed, then half-cleaners) in
+// log2(P/64R) rounds, each round's merges running in parallel across the waves with a
+// barrier between rounds.  For k <= 64R this is a fraction of the full sort's work.
+template <int NT, int R>
+__device__ __forceinline__ void block_top_desc(uint64_t* a, int P) {
   constexpr int W = NT / 64;
+  constexpr int SEG = 64 * R;
   const int l = lane_id(), w = threadIdx.x >> 6;
-  const int nseg = P >> 6;
-  for (int sg = w; sg < nseg; sg += W) a[sg * 64 + l] = wave_sort_desc<uint64_t>(a[sg * 64 + l]);
+  const int nseg = P / SEG;
+  for (int sg = w; sg < nseg; sg += W) {
+    uint64_t v[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) v[i] = a[sg * SEG + l * R + i];
+    wave_sort_desc_n<R>(v);
+#pragma unroll
+    for (int i = 0; i < R; ++i) a[sg * SEG + l * R + i] = v[i];
+  }
   __syncthreads();
   for (int step = 1; step < nseg; step <<= 1) {
     for (int m = w; m < (nseg >> 1) / step; m += W) {
       const int lo = m * 2 * step, hi = lo + step;
-      uint64_t v[1] = {a[lo * 64 + l]};
-      const uint64_t b_rev[1] = {a[hi * 64 + 63 - l]};
-      wave_merge_top<1>(v, b_rev);
-      a[lo * 64 + l] = v[0];
+      uint64_t v[R], b_rev[R];
+#pragma unroll
+      for (int i = 0; i < R; ++i) {
+        v[i] = a[lo * SEG + l * R + i];
+        b_rev[i] = a[hi * SEG + SEG - 1 - (l * R + i)];
+      }
+      wave_merge_top<R>(v, b_rev);
+#pragma unroll
+      for (int i = 0; i < R; ++i) a[lo * SEG + l * R + i] = v[i];
     }
     __syncthreads();
   }
@@ -1270,7 +1283,9 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
       while (P < total) P <<= 1;
       for (int i = total + t; i < P; i += NT) sm.top[i] = 0ull;
       __syncthreads();
-      if (keff <= 64) block_top64_desc<NT>(sm.top, P);
+      if (keff <= 64) block_top_desc<NT, 1>(sm.top, P);
+      else if (keff <= 128) block_top_desc<NT, 2>(sm.top, P);
+      else if (keff <= 256) block_top_desc<NT, 4>(sm.top, P);
       else block_bitonic_sort_desc<NT>(sm.top, P);
       sorted_in_lds = true;
     } else if (total > WSORT_MAX || wave_over) {
