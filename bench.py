@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the fused top-k + top-p sampler on one MI355X.
 
-Prints ONE JSON line.  BASELINE.json's metric has two halves and both are measured here:
+Prints ONE JSON line.  The headline metric has two halves and both are measured here:
   value          achieved logits-read bandwidth at C5 (B=256, V=151936, bf16, k=50, p=0.90),
                  cold: each step reads a different copy of the batch out of 14 rotated copies
                  (1.09 GB, more than 4x the 256 MB MALL), so the logits come from HBM;
@@ -288,7 +288,7 @@ def main() -> int:
     log(f"C1 {c1_us:.2f} us/call eager, {c1_graph_us:.2f} graph; floor {floor_us:.2f} / "
         f"{floor_graph_us:.2f}")
 
-    # the other BASELINE configs, eager back-to-back calls (hot: one buffer each)
+    # the other benchmark configurations, eager back-to-back calls (hot: one buffer each)
     others = {}
     for name in ("C2_B1_k50", "C2_B64_k50", "C3", "C4_k256", "C4_k1024"):
         c = W.case(name)

@@ -1312,6 +1312,7 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
       suffix256(sm.u.rx.hist, sm.u.rx.suf);
       __syncthreads();
       find_bucket<NT>(sm.u.rx.suf, keff, 0, &sm.misc[M_HB], &sm.misc[M_ABOVE]);
+      FSAMP_TRACE(1);
       zero_hist<NT>(sm.u.rx.hist);
       __syncthreads();
       const uint32_t hb = (uint32_t)sm.misc[M_HB];
@@ -1355,6 +1356,7 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
           }
         }
       }
+      FSAMP_TRACE(14);
       pass_barrier<CH>(kv);
       // chunk c of every thread precedes chunk c+1 in id order, and within a chunk thread t
       // precedes t+1, so a block scan per chunk ranks the tied keys by id.  `taken` is
@@ -1378,6 +1380,7 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
         }
       }
       __syncthreads();
+      FSAMP_TRACE(15);
       ncand = keff;
       regions = false;
       if (keff > WSORT_MAX) {

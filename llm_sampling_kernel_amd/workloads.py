@@ -1,8 +1,8 @@
 """Seeded synthetic inputs for the five benchmark configurations (C1-C5).
 
-The shapes, value distributions and sampling parameters are the ones BASELINE.json lists; the
-generators are numpy PCG64 streams with fixed seeds so that the same bytes are produced on the
-build container and on the GPU box.  Logits are returned as raw 16-bit patterns (uint16) plus
+The shapes, value distributions and sampling parameters are those of the five benchmark
+configurations listed below; the generators are numpy PCG64 streams with fixed seeds so that
+the same bytes are produced on the build container and on the GPU box.  Logits are returned as raw 16-bit patterns (uint16) plus
 their dtype name, because numpy has no bfloat16; ``to_bf16_bits`` rounds to nearest-even exactly
 as ``torch.Tensor.to(torch.bfloat16)`` does.
 
