@@ -187,7 +187,9 @@ typedef struct fsamp_attr_row {
   int32_t blocks_per_cu;    /* hipOccupancyMaxActiveBlocksPerMultiprocessor */
 } fsamp_attr_row;
 
-/* Writes up to max_rows rows; *n_rows receives the number of instantiations. */
+/* Writes up to max_rows rows; *n_rows receives the number of instantiations: every tiling
+ * twice, the second time (name suffix ",merge") with the workgroup hand-off and merge that
+ * calls with k > 128 and split rows launch. */
 int fsamp_kernel_attrs(fsamp_attr_row* rows, int32_t max_rows, int32_t* n_rows);
 
 /* Lane-layout self-test of the wave64 primitives the kernel is built on (DPP moves, swizzle,

@@ -162,7 +162,8 @@ int launch(const void* logits, int dtype, int64_t B, int64_t V, int64_t top_k, d
   p.stop = stop;
   p.trace = trace;
   void* args[] = {&p};
-  const hipError_t err = hipLaunchKernel(e->fn, dim3((unsigned)(B * pl.splits)), dim3(e->threads),
+  const void* fn = (pl.k > 128 && pl.splits > 1) ? e->fn_merge : e->fn;
+  const hipError_t err = hipLaunchKernel(fn, dim3((unsigned)(B * pl.splits)), dim3(e->threads),
                                          args, 0, stream);
   if (err != hipSuccess) return FSAMP_ERR_LAUNCH;
   if (hipGetLastError() != hipSuccess) return FSAMP_ERR_LAUNCH;
@@ -280,17 +281,21 @@ int fsamp_debug_sample_traced(const void* logits, int dtype, int64_t B, int64_t 
 
 int fsamp_kernel_attrs(fsamp_attr_row* rows, int32_t max_rows, int32_t* n_rows) {
   if (n_rows == nullptr) return FSAMP_ERR_NULL;
-  *n_rows = kNumKernels;
-  for (int i = 0; i < kNumKernels && i < max_rows; ++i) {
-    const KernelEntry& e = kKernels[i];
+  // every tiling twice: the common instantiation, then the one with the workgroup merge
+  *n_rows = 2 * kNumKernels;
+  for (int i = 0; i < 2 * kNumKernels && i < max_rows; ++i) {
+    const KernelEntry& e = kKernels[i % kNumKernels];
+    const bool merge = i >= kNumKernels;
+    const void* fn = merge ? e.fn_merge : e.fn;
     hipFuncAttributes a;
-    if (hipFuncGetAttributes(&a, e.fn) != hipSuccess) return FSAMP_ERR_LAUNCH;
+    if (hipFuncGetAttributes(&a, fn) != hipSuccess) return FSAMP_ERR_LAUNCH;
     int blocks = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, e.fn, e.threads, 0) != hipSuccess)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, e.threads, 0) != hipSuccess)
       return FSAMP_ERR_LAUNCH;
     fsamp_attr_row& r = rows[i];
     memset(&r, 0, sizeof(r));
     strncpy(r.name, e.name, sizeof(r.name) - 1);
+    if (merge) strncat(r.name, ",merge", sizeof(r.name) - 1 - strlen(r.name));
     r.threads = e.threads;
     r.chunks = e.chunks;
     r.vgprs = a.numRegs;

@@ -42,7 +42,8 @@ struct KernelEntry {
   int threads;
   int chunks;
   int vec;
-  const void* fn;
+  const void* fn;        // the common instantiation
+  const void* fn_merge;  // with the workgroup hand-off and merge (k > 128, split rows)
   const char* name;
 };
 

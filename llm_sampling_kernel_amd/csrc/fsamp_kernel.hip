@@ -320,6 +320,28 @@ __device__ __forceinline__ void block_bitonic_sort_desc(uint64_t* a, int P) {
   }
 }
 
+// The last level of the descending sort: a[0..P) holds a bitonic sequence (P a power of two
+// >= 64), sorted descending by the whole workgroup -- half-cleaner stages of distance >= 64
+// through LDS, then the distances below 64 in registers per 64-word segment.
+template <int NT>
+__device__ __forceinline__ void block_bitonic_merge_desc(uint64_t* a, int P) {
+  constexpr int W = NT / 64;
+  const int l = lane_id(), w = threadIdx.x >> 6;
+  for (int j = P >> 1; j >= 64; j >>= 1) {
+    for (int i = threadIdx.x; i < (P >> 1); i += NT) {
+      const int e = ((i & ~(j - 1)) << 1) | (i & (j - 1));
+      const uint64_t x = a[e], y = a[e + j];
+      if (x < y) {
+        a[e] = y;
+        a[e + j] = x;
+      }
+    }
+    __syncthreads();
+  }
+  for (int sg = w; sg < (P >> 6); sg += W) a[sg * 64 + l] = seg_merge<64, 32>(a[sg * 64 + l], true);
+  __syncthreads();
+}
+
 // The descending top 64R of a[0..P) into a[0..64R), P a power of two >= 128R, by the whole
 // workgroup: every 64R-word segment is sorted in registers by one wave (DPP network, element
 // l*R + i in lane l), then pairs of sorted segments are folded by bitonic top-merges
@@ -734,11 +756,12 @@ __device__ __forceinline__ uint32_t key_of16(uint32_t w0, uint32_t w1, uint32_t 
 template <int RB, int NT>
 __device__ __forceinline__ void wave_back_wide(const Params& p, Smem<NT>& sm, int keff, int ncand,
                                                bool sorted_in_lds, bool regions, int row,
-                                               int split, const RowCtl& rc);
+                                               int split, const RowCtl& rc, int S);
 
 template <int RB, int NT>
 __device__ __forceinline__ void wave_tail_regs(const Params& p, Smem<NT>& sm, uint64_t (&v)[RB],
-                                               int keff, int row, int split, const RowCtl& rc);
+                                               int keff, int row, int split, const RowCtl& rc,
+                                               int S);
 
 // Sorts up to 64 candidate words >= L descending, one per lane.  When every candidate key
 // lies in [L, L + 2^14) (L >= 0xC000: the slice's bound sits in the top quarter of the key
@@ -760,9 +783,9 @@ __device__ __forceinline__ uint64_t wave_sort64_words(uint64_t v, uint32_t L, in
 template <int RB, int NT>
 __device__ __forceinline__ void wave_back(const Params& p, Smem<NT>& sm, int keff, int ncand, bool sorted_in_lds,
                           bool regions, int row, int split, const RowCtl& rc, uint32_t L,
-                          uint64_t pre) {
+                          uint64_t pre, int S) {
   if constexpr (RB > 4) {
-    wave_back_wide<RB, NT>(p, sm, keff, ncand, sorted_in_lds, regions, row, split, rc);
+    wave_back_wide<RB, NT>(p, sm, keff, ncand, sorted_in_lds, regions, row, split, rc, S);
     return;
   }
   const int l = lane_id();
@@ -804,14 +827,15 @@ __device__ __forceinline__ void wave_back(const Params& p, Smem<NT>& sm, int kef
 #pragma unroll
     for (int i = 0; i < RB; ++i) v[i] = 0ull;
   }
-  wave_tail_regs<RB, NT>(p, sm, v, keff, row, split, rc);
+  wave_tail_regs<RB, NT>(p, sm, v, keff, row, split, rc, S);
 }
 
 // Wave 0 with the slice's sorted top keff in v[] (blocked by RB, zeros past keff): probe stop,
 // split hand-off and row merge when S > 1, then the ids or the sampling tail.
 template <int RB, int NT>
 __device__ __forceinline__ void wave_tail_regs(const Params& p, Smem<NT>& sm, uint64_t (&v)[RB],
-                                               int keff, int row, int split, const RowCtl& rc) {
+                                               int keff, int row, int split, const RowCtl& rc,
+                                               int S) {
   const int l = lane_id();
   FSAMP_TRACE(5);
   if (p.stop == 4) {
@@ -819,7 +843,7 @@ __device__ __forceinline__ void wave_tail_regs(const Params& p, Smem<NT>& sm, ui
     return;
   }
 
-  if (p.S > 1) {
+  if (S > 1) {
     // 5. hand the slice's sorted top-K to the row's last workgroup.  The words are written
     //    with agent-scope atomic stores, which write through to the device-coherent level,
     //    and s_waitcnt(0) holds the wave until every one of them is acknowledged before the
@@ -827,7 +851,7 @@ __device__ __forceinline__ void wave_tail_regs(const Params& p, Smem<NT>& sm, ui
     //    loads, which bypass the (per-XCD, non-coherent) L2.  That is the release / acquire
     //    pair without an L2 writeback or invalidate: on gfx950 a __threadfence costs ~1.5 us
     //    more per hand-off and the writebacks serialise across workgroups.
-    uint64_t* dst = p.partials + ((size_t)row * p.S + split) * p.K;
+    uint64_t* dst = p.partials + ((size_t)row * S + split) * p.K;
 #pragma unroll
     for (int i = 0; i < RB; ++i) {
       const int e = l * RB + i;
@@ -840,7 +864,7 @@ __device__ __forceinline__ void wave_tail_regs(const Params& p, Smem<NT>& sm, ui
                                     __HIP_MEMORY_SCOPE_AGENT);
     prev = read_lane_u32(prev, 0);
     FSAMP_TRACE(6);
-    if (prev != (unsigned)(p.S - 1)) return;
+    if (prev != (unsigned)(S - 1)) return;
     if (l == 0)
       __hip_atomic_store(&p.tickets[row * TICKET_STRIDE], 0u, __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
@@ -850,12 +874,12 @@ __device__ __forceinline__ void wave_tail_regs(const Params& p, Smem<NT>& sm, ui
     }
     // 6. merge the S sorted lists of the row: stage them in LDS (every load in flight at
     //    once), then fold them in registers
-    const int n = p.S * p.K;
-    const uint64_t* src = p.partials + (size_t)row * p.S * p.K;
+    const int n = S * p.K;
+    const uint64_t* src = p.partials + (size_t)row * S * p.K;
     load_lists(src, n, sm.g.cand);
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     FSAMP_TRACE(7);
-    wave_merge_lists<RB>(sm.g.cand, p.S, p.K, v);
+    wave_merge_lists<RB>(sm.g.cand, S, p.K, v);
     FSAMP_TRACE(8);
   }
   if (p.stop == 5 || p.stop == 6) {
@@ -873,7 +897,7 @@ __device__ __forceinline__ void wave_tail_regs(const Params& p, Smem<NT>& sm, ui
 template <int RB, int NT>
 __device__ __forceinline__ void wave_back_wide(const Params& p, Smem<NT>& sm, int keff, int ncand,
                                                bool sorted_in_lds, bool regions, int row,
-                                               int split, const RowCtl& rc) {
+                                               int split, const RowCtl& rc, int S) {
   const int l = lane_id();
   if (keff > 0 && !sorted_in_lds) {
     const uint64_t* base = regions ? sm.top : sm.g.cand;
@@ -886,9 +910,9 @@ __device__ __forceinline__ void wave_back_wide(const Params& p, Smem<NT>& sm, in
     if (l == 0 && split == 0) p.out[row] = keff > 0 ? (int64_t)unpack_id(sm.top[0]) : -1;
     return;
   }
-  if (p.S > 1) {
+  if (S > 1) {
     // hand-off and merge as in wave_back, through top[]
-    uint64_t* dst = p.partials + ((size_t)row * p.S + split) * p.K;
+    uint64_t* dst = p.partials + ((size_t)row * S + split) * p.K;
     for (int i = l; i < p.K; i += 64)
       __hip_atomic_store(&dst[i], i < keff ? sm.top[i] : 0ull, __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
@@ -899,7 +923,7 @@ __device__ __forceinline__ void wave_back_wide(const Params& p, Smem<NT>& sm, in
                                     __HIP_MEMORY_SCOPE_AGENT);
     prev = read_lane_u32(prev, 0);
     FSAMP_TRACE(6);
-    if (prev != (unsigned)(p.S - 1)) return;
+    if (prev != (unsigned)(S - 1)) return;
     if (l == 0)
       __hip_atomic_store(&p.tickets[row * TICKET_STRIDE], 0u, __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
@@ -907,12 +931,12 @@ __device__ __forceinline__ void wave_back_wide(const Params& p, Smem<NT>& sm, in
       if (l == 0) p.out[row] = (int64_t)unpack_id(sm.top[0]);
       return;
     }
-    const int n = p.S * p.K;
-    const uint64_t* src = p.partials + (size_t)row * p.S * p.K;
+    const int n = S * p.K;
+    const uint64_t* src = p.partials + (size_t)row * S * p.K;
     load_lists(src, n, sm.g.cand);
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     FSAMP_TRACE(7);
-    wave_merge_lists_dst<RB>(sm.g.cand, p.S, p.K, sm.top);
+    wave_merge_lists_dst<RB>(sm.g.cand, S, p.K, sm.top);
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     FSAMP_TRACE(8);
   }
@@ -966,7 +990,7 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
-template <int NT, int CH, bool VEC>
+template <int NT, int CH, bool VEC, bool MERGE>
 __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
   constexpr int W = NT / 64;                 // waves per workgroup
   constexpr int NP = (CH + 1) / 2;           // chunk pairs
@@ -1397,12 +1421,102 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
     }
   }
 
+  // 5-6'. Rows split over several workgroups with k > 128: the whole workgroup hands the
+  //    slice's sorted list over and, in the row's last workgroup, reads the S lists back and
+  //    folds them (workgroup bitonic merges), where one wave would take S-1 wide merges and
+  //    S*K serial loads.  The protocol is the one of the wave-0 path below: agent-scope
+  //    atomic stores, each wave waiting for its own, then one ticket for the workgroup.
+  //    Compiled only into the MERGE instantiations, which the host launches for exactly those
+  //    calls: the code would otherwise cost the common path (k <= 128) ~0.1-0.2 us.
+  bool merged = false;
+  if (MERGE && p.K > 128 && p.S > 1 && p.stop != 1 && p.stop != 2 && p.stop != 3) {
+    if (keff > 0 && !sorted_in_lds) {
+      if (wid == 0) {
+        const uint64_t* base = regions ? sm.top : sm.g.cand;
+        auto load = [&](int e) -> uint64_t { return base[e]; };
+        wave_sort_topk(load, ncand, keff, sm.top);
+      }
+      __syncthreads();
+    }
+    FSAMP_TRACE(5);
+    if (p.stop == 4) {
+      if (t == 0 && split == 0) p.out[row] = keff > 0 ? (int64_t)unpack_id(sm.top[0]) : -1;
+      return;
+    }
+    uint64_t* dst = p.partials + ((size_t)row * p.S + split) * p.K;
+    for (int i = t; i < p.K; i += NT)
+      __hip_atomic_store(&dst[i], i < keff ? sm.top[i] : 0ull, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (t == 0)
+      sm.misc[M_RED] = (int)__hip_atomic_fetch_add(&p.tickets[row * TICKET_STRIDE], 1u,
+                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    const int prev = __builtin_amdgcn_readfirstlane(sm.misc[M_RED]);
+    FSAMP_TRACE(6);
+    if (prev != p.S - 1) return;
+    if (t == 0)
+      __hip_atomic_store(&p.tickets[row * TICKET_STRIDE], 0u, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    if (p.stop == 5) {
+      if (t == 0) p.out[row] = (int64_t)unpack_id(sm.top[0]);
+      return;
+    }
+    // the S lists into cand[], four agent-scope loads in flight per thread
+    const int n = p.S * p.K;
+    const uint64_t* src = p.partials + (size_t)row * p.S * p.K;
+    for (int i0 = 0; i0 < n; i0 += 4 * NT) {
+      uint64_t w4[4];
+  #pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int i = i0 + q * NT + t;
+        w4[q] = i < n ? __hip_atomic_load(&src[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                      : 0ull;
+      }
+  #pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int i = i0 + q * NT + t;
+        if (i < n) sm.g.cand[i] = w4[q];
+      }
+    }
+    __syncthreads();
+    FSAMP_TRACE(7);
+    // top[0..P) runs the merged list (zeros past it); each further list, reversed, is folded
+    // in by an elementwise maximum (a bitonic sequence holding the top P of both) and a merge
+    int P = 64;
+    while (P < p.K) P <<= 1;
+    for (int i = t; i < P; i += NT) sm.top[i] = i < p.K ? sm.g.cand[i] : 0ull;
+    __syncthreads();
+    for (int sl = 1; sl < p.S; ++sl) {
+      for (int i = t; i < P; i += NT) {
+        const int e = P - 1 - i;
+        const uint64_t b = e < p.K ? sm.g.cand[sl * p.K + e] : 0ull;
+        const uint64_t a = sm.top[i];
+        sm.top[i] = a > b ? a : b;
+      }
+      __syncthreads();
+      block_bitonic_merge_desc<NT>(sm.top, P);
+    }
+    FSAMP_TRACE(8);
+    merged = true;
+  }
+
   // From here on wave 0 carries the workgroup alone: no more workgroup barriers.
   if (wid != 0) return;
   const RowCtl rc = row_ctl();
+  // after the workgroup merge: the row's sorted top K in top[], nothing left to hand over
+  int keff_b = keff, s_b = p.S;
+  if (merged) {
+    s_b = 1;
+    keff_b = p.K;
+    ncand = p.K;
+    sorted_in_lds = true;
+  }
   auto back = [&](auto rbc) {
     constexpr int RB = decltype(rbc)::value;
-    wave_back<RB, NT>(p, sm, keff, ncand, sorted_in_lds, regions, row, split, rc, L_sel, pre);
+    wave_back<RB, NT>(p, sm, keff_b, ncand, sorted_in_lds, regions, row, split, rc, L_sel, pre,
+                      s_b);
   };
   if (p.K <= 64) back(IC<1>{});
   else if (p.K <= 128) back(IC<2>{});
@@ -1413,10 +1527,12 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
 
 // ---- instantiation table -----------------------------------------------------------------------
 
-#define FSAMP_INST_VEC(NT_, CH_) \
-  {NT_, CH_, 1, (const void*)fsamp_kernel<NT_, CH_, true>, "fsamp_kernel<" #NT_ "," #CH_ ",vec>"},
-#define FSAMP_INST_SCALAR(NT_, CH_) \
-  {NT_, CH_, 0, (const void*)fsamp_kernel<NT_, CH_, false>, "fsamp_kernel<" #NT_ "," #CH_ ",elem>"},
+#define FSAMP_INST_VEC(NT_, CH_)                                                   \
+  {NT_, CH_, 1, (const void*)fsamp_kernel<NT_, CH_, true, false>,                  \
+   (const void*)fsamp_kernel<NT_, CH_, true, true>, "fsamp_kernel<" #NT_ "," #CH_ ",vec>"},
+#define FSAMP_INST_SCALAR(NT_, CH_)                                                \
+  {NT_, CH_, 0, (const void*)fsamp_kernel<NT_, CH_, false, false>,                 \
+   (const void*)fsamp_kernel<NT_, CH_, false, true>, "fsamp_kernel<" #NT_ "," #CH_ ",elem>"},
 
 const KernelEntry kKernels[] = {FSAMP_KERNEL_LIST_VEC(FSAMP_INST_VEC)
                                     FSAMP_KERNEL_LIST_SCALAR(FSAMP_INST_SCALAR)};
