@@ -26,16 +26,17 @@ constexpr size_t kGridCounterBytes = 256;  // the grid counter of the graph-safe
 // Tiling preference forced by fsamp_debug_force_threads (0 = automatic).
 int g_force_threads = 0;
 
-// Split count when the caller does not force one: enough workgroups to put a few hundred CUs
-// on a small batch, one workgroup per row once the batch alone fills the machine.  Each extra
-// split costs a hand-off (~3 us at B=1) and widens the row merge.
-int auto_splits(int64_t B) {
-  // Measured on MI355X (V=151936, k=50): below B=128 a call costs ~11-12 us for any S in 2..6
-  // (the post-load chain and the hand-off dominate, not bandwidth); more splits only add merge
-  // width.  From B=128 on, one workgroup per row already fills half the CUs.
+// Split count when the caller does not force one: one workgroup per row once the batch alone
+// fills half the CUs; below that, splits shorten each workgroup's selection chain (the
+// slice's candidates, gather and sort shrink with it) at the price of one more list in the
+// row merge.  Measured on MI355X (per call, k=50): V=151936 bf16 at B=1 10.35 / 10.38 /
+// 9.97 / 10.45 us for S=4/5/6/7, and with 64-value ties at B=8 16.2 / 13.4 / 12.6 us for
+// S=4/5/6; V=128256 fp16 at B=1 9.2 / 9.8 / 9.6 us for S=4/5/6 and at B=64 11.3 / 10.5 us
+// for S=2/4.
+int auto_splits(int64_t B, int64_t V) {
   if (B >= 128) return 1;
-  if (B >= 64) return 2;
-  return 4;
+  if (B >= 64) return 4;
+  return V > 131072 ? 6 : 4;
 }
 
 // Workgroup size for a slice: 256 threads while 8 chunks per thread hold it, then 512 (up to
@@ -82,7 +83,7 @@ int make_plan_impl(const void* logits, int64_t B, int64_t V, int64_t top_k, int6
   const int K = (int)pl->k;
   const bool vec = ((uintptr_t)logits % 16 == 0) && (V % 8 == 0);
   const int units = (int)((V + 7) / 8);
-  int S = splits_override > 0 ? (int)std::min<int64_t>(splits_override, 1 << 20) : auto_splits(B);
+  int S = splits_override > 0 ? (int)std::min<int64_t>(splits_override, 1 << 20) : auto_splits(B, V);
   // the row's last workgroup merges S*K words in LDS, ranking across at most MAX_SPLITS lists
   S = std::max(1, std::min({S, CAND_CAP / K, MAX_SPLITS, units}));
   const KernelEntry* e = nullptr;

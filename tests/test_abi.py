@@ -41,8 +41,8 @@ def plan(B, V, k, splits=0, ptr=4096):
 
 
 @pytest.mark.parametrize("B,V,k,S,threads", [
-    (1, 151936, 50, 4, 512),      # C1: 4 splits of 37984 elements
-    (64, 128256, 50, 2, 512),     # C2, B=64: 2 splits of 64128
+    (1, 151936, 50, 6, 512),      # C1: 6 splits of 25328 elements
+    (64, 128256, 50, 4, 512),     # C2, B=64: 4 splits of 32064
     (16, 151936, 1024, 4, 1024),  # C4 k=1024: 4 splits, 4096 merged words
     (256, 151936, 50, 1, 512),    # C5: one workgroup per row, slice in VGPRs
 ])
