@@ -17,7 +17,8 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libfsamp.so")
-SOURCES = ["fsamp_kernel.hip", "fsamp_api.hip", "fsamp_probes.hip", "fsamp_selftest.hip"]
+SOURCES = ["fsamp_kernel.hip", "fsamp_kernel_merge.hip", "fsamp_api.hip", "fsamp_probes.hip",
+           "fsamp_selftest.hip"]
 
 # -ffp-contract=off: the sampling tail's fp32 operations are evaluated exactly as written (the
 # CPU oracle mirrors them bit for bit).  Packed fp32 ops are disabled for device code.

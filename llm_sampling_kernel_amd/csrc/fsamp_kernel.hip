@@ -1526,6 +1526,37 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
 }
 
 // ---- instantiation table -----------------------------------------------------------------------
+//
+// The MERGE instantiations are compiled in their own translation unit (fsamp_kernel_merge.hip,
+// which includes this file with FSAMP_KERNEL_MERGE_TU defined), so that the two halves build in
+// parallel; here they are declared only, and the table takes their addresses.
+
+#define FSAMP_EXPLICIT_VEC(NT_, CH_) template __global__ void fsamp_kernel<NT_, CH_, true, true>(Params);
+#define FSAMP_EXPLICIT_SCALAR(NT_, CH_) \
+  template __global__ void fsamp_kernel<NT_, CH_, false, true>(Params);
+
+#ifdef FSAMP_KERNEL_MERGE_TU
+
+FSAMP_KERNEL_LIST_VEC(FSAMP_EXPLICIT_VEC)
+FSAMP_KERNEL_LIST_SCALAR(FSAMP_EXPLICIT_SCALAR)
+
+#else
+
+// the common instantiations, explicitly: the table below exists in the host pass only
+#define FSAMP_COMMON_VEC(NT_, CH_) template __global__ void fsamp_kernel<NT_, CH_, true, false>(Params);
+#define FSAMP_COMMON_SCALAR(NT_, CH_) \
+  template __global__ void fsamp_kernel<NT_, CH_, false, false>(Params);
+FSAMP_KERNEL_LIST_VEC(FSAMP_COMMON_VEC)
+FSAMP_KERNEL_LIST_SCALAR(FSAMP_COMMON_SCALAR)
+#undef FSAMP_COMMON_VEC
+#undef FSAMP_COMMON_SCALAR
+
+#define FSAMP_EXTERN_VEC(NT_, CH_) extern FSAMP_EXPLICIT_VEC(NT_, CH_)
+#define FSAMP_EXTERN_SCALAR(NT_, CH_) extern FSAMP_EXPLICIT_SCALAR(NT_, CH_)
+FSAMP_KERNEL_LIST_VEC(FSAMP_EXTERN_VEC)
+FSAMP_KERNEL_LIST_SCALAR(FSAMP_EXTERN_SCALAR)
+#undef FSAMP_EXTERN_VEC
+#undef FSAMP_EXTERN_SCALAR
 
 #define FSAMP_INST_VEC(NT_, CH_)                                                   \
   {NT_, CH_, 1, (const void*)fsamp_kernel<NT_, CH_, true, false>,                  \
@@ -1534,11 +1565,20 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
   {NT_, CH_, 0, (const void*)fsamp_kernel<NT_, CH_, false, false>,                 \
    (const void*)fsamp_kernel<NT_, CH_, false, true>, "fsamp_kernel<" #NT_ "," #CH_ ",elem>"},
 
+// host pass only: the device code of this unit does not hold the MERGE kernels the table
+// points at (their host stubs come from the other unit at link time)
+#ifndef __HIP_DEVICE_COMPILE__
 const KernelEntry kKernels[] = {FSAMP_KERNEL_LIST_VEC(FSAMP_INST_VEC)
                                     FSAMP_KERNEL_LIST_SCALAR(FSAMP_INST_SCALAR)};
 const int kNumKernels = (int)(sizeof(kKernels) / sizeof(kKernels[0]));
+#endif
 
 #undef FSAMP_INST_VEC
 #undef FSAMP_INST_SCALAR
+
+#endif  // FSAMP_KERNEL_MERGE_TU
+
+#undef FSAMP_EXPLICIT_VEC
+#undef FSAMP_EXPLICIT_SCALAR
 
 }  // namespace fsamp
