@@ -173,6 +173,21 @@ def test_candidate_sort_matches_the_oracle_on_either_side_of_its_32_bit_form(shi
     assert np.array_equal(ren.view(np.uint32), want.renormed.view(np.uint32))
 
 
+@pytest.mark.parametrize("k", [129, 200, 257, 511, 513, 1000])
+def test_split_rows_with_wide_k_merge_in_the_workgroup_exactly(k):
+    # k > 128 with split rows takes the workgroup hand-off and merge (merge widths 256, 512
+    # and 1024, k not a power of two): candidates, order, tokens and renormed bit-exact
+    bits = randn_bits((3, 151936), 95 + k, 2.0, "bfloat16")
+    x = dev(bits, "bfloat16")
+    u = ustream(3, 96)
+    want = oracle(bits, "bfloat16", k, 0.99, u)
+    for s in (0, 2, 3):
+        tok, _, keep, ren = run_u(x, k, 0.99, u, s)
+        assert np.array_equal(fused_sampling.topk_fused(x, k, s).cpu().numpy(), want.topk_ids), s
+        assert np.array_equal(tok, want.token_ids), s
+        assert np.array_equal(ren.view(np.uint32), want.renormed.view(np.uint32)), s
+
+
 def test_vocabularies_past_18_bit_ids_keep_the_exact_order():
     # ids of 2^18 and more do not fit the 32-bit sort words: those slices sort 64-bit words
     V = (1 << 18) + 4000
