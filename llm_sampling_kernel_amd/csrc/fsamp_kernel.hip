@@ -46,6 +46,16 @@ namespace fsamp {
 
 typedef short s16x2 __attribute__((ext_vector_type(2)));
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// One 16-byte load of logits with the nontemporal hint (global_load_dwordx4 ... nt): every
+// logit is read exactly once, so the lines are not worth keeping in the caches.  On MI355X a
+// 256-workgroup pass over the B=256 batch (38 such loads per thread, all issued at once)
+// measured 12.5 us with the hint against 13.9 us without it.
+__device__ __forceinline__ uint4 load_stream16(const uint16_t* a) {
+  const u32x4 r = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a));
+  return make_uint4(r.x, r.y, r.z, r.w);
+}
 
 // ---- packed 16-bit keys -----------------------------------------------------------------
 
@@ -1067,7 +1077,7 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
       for (int c = 0; c < CH; ++c) {
         const int e0 = lo + (c * NT + t) * 8;
         if constexpr (VEC) {
-          const uint4 v = *reinterpret_cast<const uint4*>(xr + min(e0, hi - 8));
+          const uint4 v = load_stream16(xr + min(e0, hi - 8));
           kv[c][0] = v.x;
           kv[c][1] = v.y;
           kv[c][2] = v.z;
