@@ -330,7 +330,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "u16+f32",
         "data": "synthetic",
         "config": {
             "workload": "C5: B=256, V=151936, bf16 logits N(0,3^2) + Zipf(1.1)-ranked bias, "
@@ -355,7 +355,8 @@ def main() -> int:
                "plan": {"splits": plan1.splits, "threads": plan1.threads,
                         "chunks": plan1.chunks}},
         "device": dev_name,
-        "compute": "u16 order keys + LDS radix/sort (integer), fp32 softmax/prefix/draw",
+        "compute": "bf16 logits in; u16 order keys and u64 (key, ~id) words for the selection "
+                   "(integer), fp32 softmax/prefix/draw",
     }
     print(json.dumps(out), flush=True)
     return 0
