@@ -263,6 +263,16 @@ def main() -> int:
     log(f"C5 cold from a HIP graph {ms_cold_graph * 1e3:.2f} us/call")
     ms_hot = median_of(c5_hot, max(200, args.steps // 4), 20, reps=3)
     log(f"C5 hot {ms_hot * 1e3:.2f} us/call")
+    # the floor: one pass over the same cold buffers (argmax per row, probes.cu's row-block scan)
+    si = [0]
+
+    def scan_cold():
+        i = si[0]
+        si[0] = i + 1
+        fused_sampling.probe_scan_rowblock(bufs[i % ROTATE])
+
+    ms_scan = timed(scan_cold, max(200, args.steps // 2), args.warmup)
+    log(f"C5 one-pass scan floor {ms_scan * 1e3:.2f} us/call")
     B5, V5 = c5.batch, c5.vocab
     gbps_cold = algo_bytes(B5, V5) / (ms_cold * 1e-3) / 1e9
     gbps_hot = algo_bytes(B5, V5) / (ms_hot * 1e-3) / 1e9
@@ -284,6 +294,9 @@ def main() -> int:
     noop = lambda: fused_sampling.probe_noop(x1)  # noqa: E731
     floor_us = median_of(noop, 5000, 200) * 1e3
     floor_graph_us = graph_per_call_ms(noop) * 1e3
+    scan1 = lambda: fused_sampling.probe_scan_rowblock(x1)  # noqa: E731
+    scan1_us = median_of(scan1, 5000, 200) * 1e3
+    scan1_graph_us = graph_per_call_ms(scan1) * 1e3
     plan1 = fused_sampling.make_plan(x1, 50)
     log(f"C1 {c1_us:.2f} us/call eager, {c1_graph_us:.2f} graph; floor {floor_us:.2f} / "
         f"{floor_graph_us:.2f}")
@@ -348,10 +361,18 @@ def main() -> int:
         "c5_cold_graph": {"us_per_call": round(ms_cold_graph * 1e3, 3),
                           "gbps": round(algo_bytes(B5, V5) / (ms_cold_graph * 1e-3) / 1e9, 1),
                           "note": "the same cold calls replayed from a HIP graph"},
+        "c5_scan_floor": {"us_per_call": round(ms_scan * 1e3, 3),
+                          "gbps": round(algo_bytes(B5, V5) / (ms_scan * 1e-3) / 1e9, 1),
+                          "note": "one pass over the same cold buffers: argmax per row, one "
+                                  "1024-thread workgroup per row, 19 nontemporal loads per "
+                                  "thread in flight, packed 16-bit key maxima, then one "
+                                  "search for the lowest index (the reference's probes.cu row-block "
+                                  "scan)"},
         "configs": others,
         "c1": {"us_per_call": round(c1_us, 3), "us_per_call_graph": round(c1_graph_us, 3),
                "launches_per_call": 1, "launch_floor_us": round(floor_us, 3),
                "launch_floor_graph_us": round(floor_graph_us, 3),
+               "scan_floor_us": round(scan1_us, 3), "scan_floor_graph_us": round(scan1_graph_us, 3),
                "plan": {"splits": plan1.splits, "threads": plan1.threads,
                         "chunks": plan1.chunks}},
         "device": dev_name,

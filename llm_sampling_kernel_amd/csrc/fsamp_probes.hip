@@ -25,24 +25,94 @@ __global__ void noop_kernel(int64_t* __restrict__ out, int n) {
   if (i < n) out[i] = 0;
 }
 
-// max of (key, ~id) over [lo, hi) of one row, one thread's share
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// One 16-byte load with the nontemporal hint, as the sampler loads its logits.
+__device__ __forceinline__ uint4 load_stream16(const uint4* a) {
+  const u32x4 r = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a));
+  return make_uint4(r.x, r.y, r.z, r.w);
+}
+
+// Vector loads a thread issues before it reduces any of them: a full row of 151,936 16-bit
+// logits is 18,992 vectors, so a 1024-thread workgroup covers it in one batch.
+constexpr int SCAN_BATCH = 19;
+
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+// Two 16-bit floats -> two order keys (the map of key16, per half, with packed 16-bit ops):
+// a negative half b becomes 0x10000 - b = (b ^ 0xFFFF) + 1, which never carries out of its
+// half; a non-negative one becomes b | 0x8000.
+__device__ __forceinline__ uint32_t keys2(uint32_t w) {
+  const s16x2 v = __builtin_bit_cast(s16x2, w);
+  const uint32_t su = __builtin_bit_cast(uint32_t, v >> (s16x2)(15));
+  return (w ^ (su | 0x80008000u)) + (su & 0x00010001u);
+}
+
+__device__ __forceinline__ uint32_t pkmax(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, a),
+                                                                __builtin_bit_cast(u16x2, b)));
+}
+
+// max of (key, ~id) over [lo, hi) of one row, one thread's share.  The vector path keeps a
+// batch of vectors as packed keys and takes their maximum with packed 16-bit maxima (about two
+// operations per element, overlapped with the loads still in flight); only a batch that
+// raises the thread's maximum is searched for the lowest index holding it.  Later batches
+// hold higher indices, so an equal maximum there never wins.
 __device__ __forceinline__ uint64_t scan_range(const uint16_t* __restrict__ row, int lo, int hi,
                                                int vec) {
   uint64_t best = 0;
   if (vec) {
     const int vlo = lo >> 3, vhi = hi >> 3;  // lo, hi multiples of 8 except the row end
     const uint4* rv = reinterpret_cast<const uint4*>(row);
-    for (int i = vlo + (int)threadIdx.x; i < vhi; i += blockDim.x) {
-      const uint4 v = rv[i];
-      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    const int step = (int)blockDim.x;
+    uint32_t best_key = 0, best_id = 0;  // key 0: nothing seen (every real value has key >= 1)
+    for (int i0 = vlo + (int)threadIdx.x; i0 < vhi; i0 += SCAN_BATCH * step) {
+      uint32_t k[SCAN_BATCH][4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const uint64_t a = pack(key16(w[q] & 0xFFFFu), (uint32_t)(i * 8 + 2 * q));
-        const uint64_t b = pack(key16(w[q] >> 16), (uint32_t)(i * 8 + 2 * q + 1));
-        best = a > best ? a : best;
-        best = b > best ? b : best;
+      for (int b = 0; b < SCAN_BATCH; ++b) {
+        const int i = i0 + b * step;
+        const uint4 v = i < vhi ? load_stream16(rv + i) : make_uint4(0u, 0u, 0u, 0u);
+        k[b][0] = v.x;
+        k[b][1] = v.y;
+        k[b][2] = v.z;
+        k[b][3] = v.w;
+      }
+      uint32_t mb[SCAN_BATCH];
+      uint32_t bmax = 0;
+#pragma unroll
+      for (int b = 0; b < SCAN_BATCH; ++b) {
+        const bool in = i0 + b * step < vhi;  // vectors past the row stay key 0
+#pragma unroll
+        for (int q = 0; q < 4; ++q) k[b][q] = in ? keys2(k[b][q]) : 0u;
+        const uint32_t m2 = pkmax(pkmax(k[b][0], k[b][1]), pkmax(k[b][2], k[b][3]));
+        mb[b] = max(m2 & 0xFFFFu, m2 >> 16);
+        bmax = max(bmax, mb[b]);
+      }
+      if (bmax > best_key) {
+        // the first vector of the batch that holds bmax (scanning down leaves the first),
+        // then the first of its eight elements that does
+        int fb = 0;
+        uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int b = SCAN_BATCH - 1; b >= 0; --b) {
+          if (mb[b] == bmax) {
+            fb = b;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) w[q] = k[b][q];
+          }
+        }
+        int j = 0;
+#pragma unroll
+        for (int e = 7; e >= 0; --e) {
+          const uint32_t key = (e & 1) ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xFFFFu);
+          if (key == bmax) j = e;
+        }
+        best_key = bmax;
+        best_id = (uint32_t)((i0 + fb * step) * 8 + j);
       }
     }
+    if (best_key != 0u) best = pack(best_key, best_id);
     for (int i = vhi * 8 + (int)threadIdx.x; i < hi; i += blockDim.x) {
       const uint64_t a = pack(key16(row[i]), (uint32_t)i);
       best = a > best ? a : best;

@@ -481,6 +481,17 @@ def test_floor_probes_return_the_argmax():
     assert fused_sampling.probe_noop(x).shape == (8,)
 
 
+@pytest.mark.parametrize("V", [1000, 8 * 1024 * 19 + 8, 128256, 151937])
+def test_floor_scan_probe_batches_and_row_ends(V):
+    # rows shorter than one batch of vector loads, one vector past a full batch, the C2 row, and
+    # a row that is not a multiple of 8 (element loads)
+    bits = randn_bits((3, V), 93, 2.0, "float16")
+    x = dev(bits, "float16")
+    want = x.float().argmax(-1)
+    assert torch.equal(fused_sampling.probe_scan_rowblock(x), want)
+    assert torch.equal(fused_sampling.probe_scan_split(x, 3), want)
+
+
 def test_kernel_attrs_report_every_instantiation_without_spills_in_the_planned_tilings():
     rows = fused_sampling.kernel_attrs()
     assert len(rows) >= 20
