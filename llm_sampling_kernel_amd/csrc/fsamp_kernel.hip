@@ -1211,12 +1211,19 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
       return ge_mask(ka, L) | (ge_mask(kb, L) << 8);
     };
     int mine = 0;
+    // the staged slots' masks, kept for the write pass: the LDS atomic between the two passes
+    // would otherwise make the compiler read the staged copies again
+    uint32_t smask[STAGE_SLOTS];
     if (from_regs) {
 #pragma unroll
       for (int c = C0; c < C1; ++c)
         if (pair_ge(c, L)) mine += __popc(ge_mask(kv[c], L));
     } else {
-      for (int s = 0; s < nst; ++s) mine += __popc(staged_mask(s));
+#pragma unroll
+      for (int s = 0; s < STAGE_SLOTS; ++s) {
+        smask[s] = s < nst ? staged_mask(s) : 0u;
+        mine += __popc(smask[s]);
+      }
     }
     FSAMP_TRACE(10);
     if (__ballot(mine > 0) != 0ull) {
@@ -1243,8 +1250,10 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
         }
       } else {
         const uint32_t idb = opaque_base(lo, t);
-        for (int s = 0; s < nst; ++s) {
-          uint32_t m = staged_mask(s);
+#pragma unroll
+        for (int s = 0; s < STAGE_SLOTS; ++s) {
+          uint32_t m = smask[s];
+          if (m == 0u) continue;
           const int c0 = 2 * (int)sm.meta[s][t];
           const uint16_t* ka = reinterpret_cast<const uint16_t*>(&sm.g.st.a[s][t]);
           const uint16_t* kb = reinterpret_cast<const uint16_t*>(&sm.g.st.b[s][t]);
