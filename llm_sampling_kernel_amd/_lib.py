@@ -55,6 +55,7 @@ SIGNATURES = {
     "fsamp_probe_noop": (_i32, [_i64, _vp, _vp]),
     "fsamp_probe_scan_rowblock": (_i32, [_vp, _i32, _i64, _i64, _vp, _vp]),
     "fsamp_probe_scan_split": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _sz, _vp]),
+    "fsamp_probe_load": (_i32, [_vp, _i32, _i64, _i64, _vp, _vp]),
     "fsamp_kernel_attrs": (_i32, [ctypes.POINTER(AttrRow), _i32, ctypes.POINTER(_i32)]),
     "fsamp_debug_force_threads": (_i32, [_i32]),
     "fsamp_debug_wave_selftest": (_i32, [_vp, _vp]),

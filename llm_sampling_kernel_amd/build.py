@@ -17,8 +17,12 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libfsamp.so")
-SOURCES = ["fsamp_kernel.hip", "fsamp_kernel_merge.hip", "fsamp_api.hip", "fsamp_probes.hip",
-           "fsamp_selftest.hip"]
+# (source, object, extra flags): the sampler kernel is compiled in eight parts plus its table
+# (fsamp_kernel.hip, FSAMP_PART), so that the instantiations build in parallel
+SOURCES = ([("fsamp_kernel.hip", f"fsamp_kernel_part{n}.o", [f"-DFSAMP_PART={n}"]) for n in range(8)]
+           + [("fsamp_kernel.hip", "fsamp_kernel_table.o", []),
+              ("fsamp_api.hip", "fsamp_api.o", []), ("fsamp_probes.hip", "fsamp_probes.o", []),
+              ("fsamp_selftest.hip", "fsamp_selftest.o", [])])
 
 # -ffp-contract=off: the sampling tail's fp32 operations are evaluated exactly as written (the
 # CPU oracle mirrors them bit for bit).  Packed fp32 ops are disabled for device code.
@@ -42,13 +46,13 @@ def build(verbose: bool = False) -> str:
     cc = hipcc()
     procs = []
     objs = []
-    for src in SOURCES:
-        obj = os.path.join(BUILD, src.replace(".hip", ".o"))
+    for src, oname, extra in SOURCES:
+        obj = os.path.join(BUILD, oname)
         objs.append(obj)
-        cmd = [cc, *HIPCC_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+        cmd = [cc, *HIPCC_FLAGS, *extra, "-c", os.path.join(CSRC, src), "-o", obj]
         if verbose:
             print(" ".join(cmd), flush=True)
-        procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
+        procs.append((oname, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
                                             text=True)))
     failed = []
     for src, p in procs:

@@ -48,11 +48,16 @@ struct KernelEntry {
 };
 
 // (threads, chunks) register tilings that are compiled; chunks*8 elements per thread.
-// Vector-load (16-byte aligned rows) tilings:
-#define FSAMP_KERNEL_LIST_VEC(X) \
-  X(256, 1) X(256, 2) X(256, 3) X(256, 4) X(256, 5) X(256, 6) X(256, 8) X(256, 12) X(256, 16) \
-  X(512, 8) X(512, 12) X(512, 16) X(512, 20) X(512, 24) X(512, 32) X(512, 38) \
+// Vector-load (16-byte aligned rows) tilings, by workgroup size (each group is compiled in its
+// own parts of the build, see fsamp_kernel.hip):
+#define FSAMP_KERNEL_LIST_VEC_256(X) \
+  X(256, 1) X(256, 2) X(256, 3) X(256, 4) X(256, 5) X(256, 6) X(256, 8) X(256, 12) X(256, 16)
+#define FSAMP_KERNEL_LIST_VEC_512(X) \
+  X(512, 8) X(512, 12) X(512, 16) X(512, 20) X(512, 24) X(512, 32) X(512, 38)
+#define FSAMP_KERNEL_LIST_VEC_1024(X) \
   X(1024, 4) X(1024, 5) X(1024, 6) X(1024, 8) X(1024, 10) X(1024, 12) X(1024, 16) X(1024, 19)
+#define FSAMP_KERNEL_LIST_VEC(X) \
+  FSAMP_KERNEL_LIST_VEC_256(X) FSAMP_KERNEL_LIST_VEC_512(X) FSAMP_KERNEL_LIST_VEC_1024(X)
 // Element-load tilings (rows not 16-byte aligned, V % 8 != 0): small slices only; the planner
 // adds splits until a slice fits.
 #define FSAMP_KERNEL_LIST_SCALAR(X) \

@@ -1546,36 +1546,50 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
 
 // ---- instantiation table -----------------------------------------------------------------------
 //
-// The MERGE instantiations are compiled in their own translation unit (fsamp_kernel_merge.hip,
-// which includes this file with FSAMP_KERNEL_MERGE_TU defined), so that the two halves build in
-// parallel; here they are declared only, and the table takes their addresses.
+// The instantiations are compiled in eight parts, in parallel: this file built with
+// -DFSAMP_PART=n (n = 0..7) instantiates one group of tilings, common (n even) or MERGE (n odd),
+// and the build without FSAMP_PART holds only the host-side table, which takes the addresses of
+// every instantiation (their host stubs come from the parts at link time).
 
-#define FSAMP_EXPLICIT_VEC(NT_, CH_) template __global__ void fsamp_kernel<NT_, CH_, true, true>(Params);
-#define FSAMP_EXPLICIT_SCALAR(NT_, CH_) \
-  template __global__ void fsamp_kernel<NT_, CH_, false, true>(Params);
-
-#ifdef FSAMP_KERNEL_MERGE_TU
-
-FSAMP_KERNEL_LIST_VEC(FSAMP_EXPLICIT_VEC)
-FSAMP_KERNEL_LIST_SCALAR(FSAMP_EXPLICIT_SCALAR)
-
-#else
-
-// the common instantiations, explicitly: the table below exists in the host pass only
 #define FSAMP_COMMON_VEC(NT_, CH_) template __global__ void fsamp_kernel<NT_, CH_, true, false>(Params);
 #define FSAMP_COMMON_SCALAR(NT_, CH_) \
   template __global__ void fsamp_kernel<NT_, CH_, false, false>(Params);
-FSAMP_KERNEL_LIST_VEC(FSAMP_COMMON_VEC)
-FSAMP_KERNEL_LIST_SCALAR(FSAMP_COMMON_SCALAR)
-#undef FSAMP_COMMON_VEC
-#undef FSAMP_COMMON_SCALAR
+#define FSAMP_MERGE_VEC(NT_, CH_) template __global__ void fsamp_kernel<NT_, CH_, true, true>(Params);
+#define FSAMP_MERGE_SCALAR(NT_, CH_) \
+  template __global__ void fsamp_kernel<NT_, CH_, false, true>(Params);
 
-#define FSAMP_EXTERN_VEC(NT_, CH_) extern FSAMP_EXPLICIT_VEC(NT_, CH_)
-#define FSAMP_EXTERN_SCALAR(NT_, CH_) extern FSAMP_EXPLICIT_SCALAR(NT_, CH_)
-FSAMP_KERNEL_LIST_VEC(FSAMP_EXTERN_VEC)
-FSAMP_KERNEL_LIST_SCALAR(FSAMP_EXTERN_SCALAR)
-#undef FSAMP_EXTERN_VEC
-#undef FSAMP_EXTERN_SCALAR
+#if defined(FSAMP_PART)
+
+#if FSAMP_PART == 0
+FSAMP_KERNEL_LIST_VEC_256(FSAMP_COMMON_VEC)
+#elif FSAMP_PART == 1
+FSAMP_KERNEL_LIST_VEC_256(FSAMP_MERGE_VEC)
+#elif FSAMP_PART == 2
+FSAMP_KERNEL_LIST_VEC_512(FSAMP_COMMON_VEC)
+#elif FSAMP_PART == 3
+FSAMP_KERNEL_LIST_VEC_512(FSAMP_MERGE_VEC)
+#elif FSAMP_PART == 4
+FSAMP_KERNEL_LIST_VEC_1024(FSAMP_COMMON_VEC)
+#elif FSAMP_PART == 5
+FSAMP_KERNEL_LIST_VEC_1024(FSAMP_MERGE_VEC)
+#elif FSAMP_PART == 6
+FSAMP_KERNEL_LIST_SCALAR(FSAMP_COMMON_SCALAR)
+#elif FSAMP_PART == 7
+FSAMP_KERNEL_LIST_SCALAR(FSAMP_MERGE_SCALAR)
+#else
+#error "FSAMP_PART must be in [0, 7]"
+#endif
+
+#else  // the table
+
+#define FSAMP_EXTERN_COMMON_VEC(NT_, CH_) extern FSAMP_COMMON_VEC(NT_, CH_)
+#define FSAMP_EXTERN_COMMON_SCALAR(NT_, CH_) extern FSAMP_COMMON_SCALAR(NT_, CH_)
+#define FSAMP_EXTERN_MERGE_VEC(NT_, CH_) extern FSAMP_MERGE_VEC(NT_, CH_)
+#define FSAMP_EXTERN_MERGE_SCALAR(NT_, CH_) extern FSAMP_MERGE_SCALAR(NT_, CH_)
+FSAMP_KERNEL_LIST_VEC(FSAMP_EXTERN_COMMON_VEC)
+FSAMP_KERNEL_LIST_SCALAR(FSAMP_EXTERN_COMMON_SCALAR)
+FSAMP_KERNEL_LIST_VEC(FSAMP_EXTERN_MERGE_VEC)
+FSAMP_KERNEL_LIST_SCALAR(FSAMP_EXTERN_MERGE_SCALAR)
 
 #define FSAMP_INST_VEC(NT_, CH_)                                                   \
   {NT_, CH_, 1, (const void*)fsamp_kernel<NT_, CH_, true, false>,                  \
@@ -1584,20 +1598,13 @@ FSAMP_KERNEL_LIST_SCALAR(FSAMP_EXTERN_SCALAR)
   {NT_, CH_, 0, (const void*)fsamp_kernel<NT_, CH_, false, false>,                 \
    (const void*)fsamp_kernel<NT_, CH_, false, true>, "fsamp_kernel<" #NT_ "," #CH_ ",elem>"},
 
-// host pass only: the device code of this unit does not hold the MERGE kernels the table
-// points at (their host stubs come from the other unit at link time)
+// host pass only: the device code of this unit holds no instantiation
 #ifndef __HIP_DEVICE_COMPILE__
 const KernelEntry kKernels[] = {FSAMP_KERNEL_LIST_VEC(FSAMP_INST_VEC)
                                     FSAMP_KERNEL_LIST_SCALAR(FSAMP_INST_SCALAR)};
 const int kNumKernels = (int)(sizeof(kKernels) / sizeof(kKernels[0]));
 #endif
 
-#undef FSAMP_INST_VEC
-#undef FSAMP_INST_SCALAR
-
-#endif  // FSAMP_KERNEL_MERGE_TU
-
-#undef FSAMP_EXPLICIT_VEC
-#undef FSAMP_EXPLICIT_SCALAR
+#endif  // FSAMP_PART
 
 }  // namespace fsamp

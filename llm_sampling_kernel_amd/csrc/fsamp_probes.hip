@@ -1,6 +1,7 @@
 // fsamp_probes.hip -- floor probes that bound the sampler from below on the same instrument
 // (csrc/probes.cu:6-125 in the reference): an empty launch, one full argmax pass with one
-// workgroup per row, and a split-row argmax pass plus a per-row merge.
+// workgroup per row, and a split-row argmax pass plus a per-row merge; plus a load-only pass in
+// the sampler's B=256 launch shape (no counterpart in the reference).
 
 #include <hip/hip_runtime.h>
 
@@ -180,6 +181,42 @@ __global__ __launch_bounds__(64) void merge_partial_kernel(const uint64_t* __res
   if (threadIdx.x == 0) out[blockIdx.x] = (int64_t)(0xFFFFFFFFu - (uint32_t)best);
 }
 
+// Load-only floor of the sampler's B=256 launch shape: one 512-thread workgroup per row, every
+// thread issues its LOAD_CH nontemporal dwordx4 loads at once (chunk c of thread t at vector
+// c*512 + t, as the sampler lays its slice out), converts them to packed order keys and keeps
+// their packed maximum; each wave then writes the maximum key of its share (no barrier, no LDS),
+// so the kernel's time is the row read itself plus the launch.
+constexpr int LOAD_NT = 512, LOAD_CH = 38;
+
+__global__ __launch_bounds__(LOAD_NT) void load_rows_kernel(const uint16_t* __restrict__ x,
+                                                            uint32_t* __restrict__ wave_max,
+                                                            int V) {
+  const uint4* rv = reinterpret_cast<const uint4*>(x + (size_t)blockIdx.x * V);
+  const int nvec = V >> 3;
+  const int t = threadIdx.x;
+  uint32_t k[LOAD_CH][4];
+#pragma unroll
+  for (int c = 0; c < LOAD_CH; ++c) {
+    const int i = c * LOAD_NT + t;
+    const uint4 v = load_stream16(rv + min(i, nvec - 1));
+    k[c][0] = v.x;
+    k[c][1] = v.y;
+    k[c][2] = v.z;
+    k[c][3] = v.w;
+  }
+  uint32_t m = 0;
+#pragma unroll
+  for (int c = 0; c < LOAD_CH; ++c) {
+    const bool in = c * LOAD_NT + t < nvec;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) m = pkmax(m, in ? keys2(k[c][q]) : 0u);
+  }
+  uint32_t mk = max(m & 0xFFFFu, m >> 16);
+#pragma unroll
+  for (int d = 32; d > 0; d >>= 1) mk = max(mk, (uint32_t)__shfl_xor((int)mk, d, 64));
+  if ((t & 63) == 0) wave_max[(size_t)blockIdx.x * (LOAD_NT / 64) + (t >> 6)] = mk;
+}
+
 int check(int dtype, int64_t B, int64_t V) {
   if (dtype != FSAMP_DTYPE_F16 && dtype != FSAMP_DTYPE_BF16) return FSAMP_ERR_DTYPE;
   if (B < 1 || V < 1 || V > (int64_t)0x7FFFFFF0 || B > (int64_t)0x7FFFFFFF) return FSAMP_ERR_SHAPE;
@@ -205,6 +242,18 @@ int fsamp_probe_scan_rowblock(const void* logits, int dtype, int64_t B, int64_t 
   const int vec = ((uintptr_t)logits % 16 == 0) && (V % 8 == 0);
   hipLaunchKernelGGL(scan_rowblock_kernel, dim3((unsigned)B), dim3(1024), 0, stream,
                      static_cast<const uint16_t*>(logits), out, (int)V, vec);
+  return hipGetLastError() == hipSuccess ? FSAMP_OK : FSAMP_ERR_LAUNCH;
+}
+
+int fsamp_probe_load(const void* logits, int dtype, int64_t B, int64_t V, uint32_t* wave_max,
+                     hipStream_t stream) {
+  const int rc = check(dtype, B, V);
+  if (rc != FSAMP_OK) return rc;
+  if (logits == nullptr || wave_max == nullptr) return FSAMP_ERR_NULL;
+  if ((uintptr_t)logits % 16 != 0 || V % 8 != 0 || V > (int64_t)LOAD_NT * LOAD_CH * 8)
+    return FSAMP_ERR_VOCAB;
+  hipLaunchKernelGGL(load_rows_kernel, dim3((unsigned)B), dim3(LOAD_NT), 0, stream,
+                     static_cast<const uint16_t*>(logits), wave_max, (int)V);
   return hipGetLastError() == hipSuccess ? FSAMP_OK : FSAMP_ERR_LAUNCH;
 }
 

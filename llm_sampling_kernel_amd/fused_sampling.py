@@ -292,6 +292,22 @@ def probe_scan_rowblock(logits: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def probe_load(logits: torch.Tensor, wave_max: torch.Tensor | None = None) -> torch.Tensor:
+    """Load-only floor in the sampler's B=256 launch shape: [B, 8] int32 per-wave maximum order
+    keys (fsamp_probe_load).  No counterpart in the reference."""
+    dtype = _check_logits(logits)
+    B, V = logits.shape
+    if wave_max is None:
+        wave_max = torch.empty(B * 8, dtype=torch.int32, device=logits.device)
+    if not (wave_max.is_cuda and wave_max.dtype == torch.int32 and wave_max.numel() >= B * 8
+            and wave_max.is_contiguous()):
+        raise RuntimeError("wave_max must be a contiguous int32 cuda tensor of B*8 entries")
+    _lib.check(_lib.load().fsamp_probe_load(ctypes.c_void_p(logits.data_ptr()), dtype, B, V,
+                                            ctypes.c_void_p(wave_max.data_ptr()),
+                                            ctypes.c_void_p(_stream_ptr(logits.device))))
+    return wave_max[:B * 8].view(B, 8)
+
+
 def probe_scan_split(logits: torch.Tensor, splits: int) -> torch.Tensor:
     """One full pass split over `splits` workgroups per row, then a merge (:108-125)."""
     dtype = _check_logits(logits)

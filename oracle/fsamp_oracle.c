@@ -197,6 +197,30 @@ static void stable_desc_order32(const float* row, int64_t V, vid_t* tmp, int32_t
   for (int64_t i = 0; i < V; ++i) order[i] = tmp[i].id;
 }
 
+/* The reference's own form of the selection, reference.py:48-54: the row converted to fp32
+ * (x.to(float32)) and fully sorted, descending, by a stable sort -- here a bottom-up merge
+ * sort of (value, id) pairs, O(V log V).  Runs are merged taking the left element while it is
+ * not smaller, so equal values (and -0 == +0, as fp32 compares them) keep ascending ids.  Used
+ * for the CPU baseline in the reference's form and to cross-check the counting sort above. */
+static void stable_desc_order_merge(vid_t* a, vid_t* b, int64_t V, int32_t* order) {
+  vid_t* src = a;
+  vid_t* dst = b;
+  for (int64_t w = 1; w < V; w <<= 1) {
+    for (int64_t lo = 0; lo < V; lo += 2 * w) {
+      const int64_t mid = lo + w < V ? lo + w : V;
+      const int64_t hi = lo + 2 * w < V ? lo + 2 * w : V;
+      int64_t i = lo, j = mid, o = lo;
+      while (i < mid && j < hi) dst[o++] = (src[i].v >= src[j].v) ? src[i++] : src[j++];
+      while (i < mid) dst[o++] = src[i++];
+      while (j < hi) dst[o++] = src[j++];
+    }
+    vid_t* t = src;
+    src = dst;
+    dst = t;
+  }
+  for (int64_t i = 0; i < V; ++i) order[i] = src[i].id;
+}
+
 /* ---- fp32 tail in the fixed lane order --------------------------------------------------- */
 
 typedef struct {
@@ -304,11 +328,12 @@ static tail_out_t tail_f32(const float* x, int K, double top_p, float u, float i
  * Stage outputs stay [B, K] with K = min(top_k, V); ranks past a row's own k are 0, and
  * probs / cumsum there are 0 as well.
  */
-int oracle_sample_rows(const void* logits, int dtype, int64_t B, int64_t V, int64_t top_k,
-                       double top_p, const float* u, const int32_t* topk_row,
-                       const float* topp_row, const float* temp_row, int64_t* token_ids,
-                       int64_t* topk_ids, float* topk_vals, float* probs, float* cumsum,
-                       uint8_t* keep, float* renormed, int32_t* cutoff, int nthreads) {
+static int sample_rows_impl(const void* logits, int dtype, int64_t B, int64_t V, int64_t top_k,
+                            double top_p, const float* u, const int32_t* topk_row,
+                            const float* topp_row, const float* temp_row, int64_t* token_ids,
+                            int64_t* topk_ids, float* topk_vals, float* probs, float* cumsum,
+                            uint8_t* keep, float* renormed, int32_t* cutoff, int nthreads,
+                            int full_sort) {
   if (B < 0 || V < 1 || top_k < 1 || !(top_p > 0.0 && top_p <= 1.0) || u == NULL ||
       token_ids == NULL || (dtype != OR_F16 && dtype != OR_BF16 && dtype != OR_F32))
     return OR_BADARG;
@@ -320,13 +345,24 @@ int oracle_sample_rows(const void* logits, int dtype, int64_t B, int64_t V, int6
 #endif
   for (int64_t b = 0; b < B; ++b) {
     int32_t* order = (int32_t*)malloc((size_t)V * sizeof(int32_t));
-    uint32_t* counts = dtype == OR_F32 ? NULL : (uint32_t*)malloc(65536 * sizeof(uint32_t));
-    vid_t* tmp = dtype == OR_F32 ? (vid_t*)malloc((size_t)V * sizeof(vid_t)) : NULL;
+    const int use_counts = dtype != OR_F32 && !full_sort;
+    uint32_t* counts = use_counts ? (uint32_t*)malloc(65536 * sizeof(uint32_t)) : NULL;
+    vid_t* tmp = use_counts ? NULL : (vid_t*)malloc((size_t)V * 2 * sizeof(vid_t));
     float* x = (float*)malloc((size_t)K * 4 * sizeof(float));
-    if (!order || (dtype != OR_F32 && !counts) || (dtype == OR_F32 && !tmp) || !x) {
+    if (!order || (use_counts && !counts) || (!use_counts && !tmp) || !x) {
       status = OR_NOMEM;
     } else {
-      if (dtype == OR_F32) {
+      if (full_sort) {
+        for (int64_t i = 0; i < V; ++i) {
+          tmp[i].v = dtype == OR_F32 ? ((const float*)logits)[b * V + i]
+                                     : oracle_to_float(((const uint16_t*)logits)[b * V + i], dtype);
+          tmp[i].id = (int32_t)i;
+        }
+        stable_desc_order_merge(tmp, tmp + V, V, order);
+        for (int64_t j = 0; j < K; ++j)
+          x[j] = dtype == OR_F32 ? ((const float*)logits)[b * V + order[j]]
+                                 : oracle_to_float(((const uint16_t*)logits)[b * V + order[j]], dtype);
+      } else if (dtype == OR_F32) {
         const float* row = (const float*)logits + b * V;
         stable_desc_order32(row, V, tmp, order);
         for (int64_t j = 0; j < K; ++j) x[j] = row[order[j]];
@@ -368,6 +404,29 @@ int oracle_sample_rows(const void* logits, int dtype, int64_t B, int64_t V, int6
     free(x);
   }
   return status;
+}
+
+int oracle_sample_rows(const void* logits, int dtype, int64_t B, int64_t V, int64_t top_k,
+                       double top_p, const float* u, const int32_t* topk_row,
+                       const float* topp_row, const float* temp_row, int64_t* token_ids,
+                       int64_t* topk_ids, float* topk_vals, float* probs, float* cumsum,
+                       uint8_t* keep, float* renormed, int32_t* cutoff, int nthreads) {
+  return sample_rows_impl(logits, dtype, B, V, top_k, top_p, u, topk_row, topp_row, temp_row,
+                          token_ids, topk_ids, topk_vals, probs, cumsum, keep, renormed, cutoff,
+                          nthreads, 0);
+}
+
+/*
+ * oracle_sample_fullsort: oracle_sample with the selection in the reference's own form
+ * (reference.py:48-54): each row converted to fp32 and fully sorted by a stable merge sort
+ * (stable_desc_order_merge), then the same fp32 tail.  Same outputs as oracle_sample; this is
+ * the O(V log V) path the CPU baseline times.
+ */
+int oracle_sample_fullsort(const void* logits, int dtype, int64_t B, int64_t V, int64_t top_k,
+                           double top_p, const float* u, int64_t* token_ids, int64_t* topk_ids,
+                           int nthreads) {
+  return sample_rows_impl(logits, dtype, B, V, top_k, top_p, u, NULL, NULL, NULL, token_ids,
+                          topk_ids, NULL, NULL, NULL, NULL, NULL, NULL, nthreads, 1);
 }
 
 int oracle_sample(const void* logits, int dtype, int64_t B, int64_t V, int64_t top_k,

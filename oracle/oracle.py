@@ -44,6 +44,8 @@ def lib():
         L.oracle_sample_rows.argtypes = [vp, i32, i64, i64, i64, dbl, vp, vp, vp, vp, vp, vp, vp,
                                          vp, vp, vp, vp, vp, i32]
         L.oracle_sample_rows.restype = i32
+        L.oracle_sample_fullsort.argtypes = [vp, i32, i64, i64, i64, dbl, vp, vp, vp, i32]
+        L.oracle_sample_fullsort.restype = i32
         L.oracle_stages_f64.argtypes = [vp, i32, i64, i64, i64, dbl, vp, vp, vp, vp]
         L.oracle_stages_f64.restype = i32
         L.oracle_stages_f64_t.argtypes = [vp, i32, i64, i64, i64, dbl, dbl, vp, vp, vp, vp]
@@ -138,6 +140,26 @@ def sample(x: np.ndarray, dtype: str, top_k: int, top_p: float, u: np.ndarray, *
     if not return_stages:
         return tok
     return Stages(ids, vals, probs, cum, keep.astype(bool), cutoff, ren, tok)
+
+
+def sample_fullsort(x: np.ndarray, dtype: str, top_k: int, top_p: float, u: np.ndarray, *,
+                    nthreads: int = 1):
+    """sample() with the selection in the reference's own form (reference.py:48-54): each row
+    converted to fp32 and fully sorted by a stable merge sort, O(V log V), instead of the
+    counting sort.  Returns (token_ids [B], topk_ids [B,K]); no input validation."""
+    x = _logits(x, dtype)
+    if top_k < 1 or not 0.0 < top_p <= 1.0:
+        raise ValueError("top_k must be >= 1 and top_p in (0, 1]")
+    B, V = x.shape
+    K = min(int(top_k), V)
+    u = np.ascontiguousarray(u, dtype=np.float32).reshape(B)
+    tok = np.empty(B, np.int64)
+    ids = np.empty((B, K), np.int64)
+    rc = lib().oracle_sample_fullsort(_ptr(x), DTYPES[dtype], B, V, int(top_k), float(top_p),
+                                      _ptr(u), _ptr(tok), _ptr(ids), int(nthreads))
+    if rc != 0:
+        raise RuntimeError(f"oracle_sample_fullsort failed ({rc})")
+    return tok, ids
 
 
 def stages_f64(x: np.ndarray, dtype: str, top_k: int, top_p: float, temperature: float = 1.0):

@@ -381,11 +381,14 @@ def test_workspace_is_reused_safely_across_batch_sizes():
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("batch", [1, 8])
 def test_the_last_ablation_phase_is_the_production_path(batch, dtype):
-    x = dev(randn_bits((batch, 4000), 58 + batch, 4.0, dtype), dtype)
+    # phase 7 is the whole sampler with seed = offset = 0: the oracle's tokens for the
+    # splitmix64 uniforms of (0, 0, row)
+    bits = randn_bits((batch, 4000), 58 + batch, 4.0, dtype)
+    x = dev(bits, dtype)
+    u = O.rng_uniform(0, 0, batch)
     for top_k in (20, 50):
-        got = fused_sampling.probe_phase(x, top_k, 0.9, 7, 0)
-        want = fused_sampling.sample_fused(x, top_k, 0.9, 0, 0, 0)
-        assert torch.equal(got, want)
+        got = fused_sampling.probe_phase(x, top_k, 0.9, 7, 0).cpu().numpy()
+        assert np.array_equal(got, oracle(bits, dtype, top_k, 0.9, u).token_ids)
 
 
 def test_early_ablation_phases_stop_before_the_answer_exists():
@@ -490,6 +493,18 @@ def test_floor_scan_probe_batches_and_row_ends(V):
     want = x.float().argmax(-1)
     assert torch.equal(fused_sampling.probe_scan_rowblock(x), want)
     assert torch.equal(fused_sampling.probe_scan_split(x, 3), want)
+
+
+@pytest.mark.parametrize("V", [151936, 128256, 1000])
+def test_load_floor_probe_reads_each_waves_share(V):
+    # wave w of the 512-thread workgroup owns vectors c*512 + 64w .. c*512 + 64w + 63
+    bits = randn_bits((5, V), 94, 3.0, "bfloat16")
+    got = fused_sampling.probe_load(dev(bits, "bfloat16")).cpu().numpy().view(np.uint32)
+    keys = O.key16(bits).reshape(5, V // 8, 8).max(axis=2)
+    owner = (np.arange(V // 8) % 512) // 64
+    want = np.stack([keys[:, owner == w].max(axis=1) if (owner == w).any()
+                     else np.zeros(5, np.uint32) for w in range(8)], axis=1)
+    assert np.array_equal(got, want)
 
 
 def test_kernel_attrs_report_every_instantiation_without_spills_in_the_planned_tilings():

@@ -140,6 +140,27 @@ def test_topk_matches_numpy_stable_argsort(dtype, scale, k):
     assert np.array_equal(s.topk_ids, brute_topk(xin, dtype, min(k, 5000)))
 
 
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+@pytest.mark.parametrize("k", [1, 50, 1024])
+def test_counting_sort_selection_equals_the_reference_form_full_sort(dtype, k):
+    # the reference's own selection (reference.py:48-54: fp32 conversion + full stable sort),
+    # restated as a merge sort, against the counting sort the oracle uses: ties, +-0, a
+    # dense grid of repeated values and -inf tails must all come out the same, and so must the
+    # token drawn from the same u
+    x = randn((6, 6000), 23, 3.0)
+    x[0, ::5] = 0.0
+    x[1, 1::3] = -0.0
+    x[2, :] = np.linspace(-8, 8, 64, dtype=np.float32)[np.arange(6000) % 64]
+    x[3, 50:] = -np.inf
+    x[4, :] = 1.5
+    bits = W.to_bits(x, dtype)
+    u = np.linspace(0.01, 0.99, 6, dtype=np.float32)
+    s = stages(bits, dtype, k, 0.9, u)
+    tok, ids = O.sample_fullsort(bits, dtype, k, 0.9, u, nthreads=4)
+    assert np.array_equal(ids, s.topk_ids)
+    assert np.array_equal(tok, s.token_ids)
+
+
 def test_plus_and_minus_zero_tie_and_resolve_by_id():
     bits = np.array([[0x8000, 0x0000, 0x8000, 0x3F80, 0x0000]], np.uint16)  # -0 +0 -0 1 +0
     s = stages(bits, "bfloat16", 5, 1.0)
