@@ -52,7 +52,8 @@ enum fsamp_status {
   FSAMP_ERR_PHASE = 8,      /* "phase must be in [1, 7]" */
   FSAMP_ERR_SPLITS = 9,     /* "splits must be >= 1" (probe) */
   FSAMP_ERR_VOCAB = 10,     /* vocabulary does not fit the workgroup tiling */
-  FSAMP_ERR_LAUNCH = 11     /* the HIP runtime reported an error at launch */
+  FSAMP_ERR_LAUNCH = 11,    /* the HIP runtime reported an error at launch */
+  FSAMP_ERR_VERSION = 12    /* fsamp_call.struct_bytes is not sizeof(fsamp_call) */
 };
 
 #define FSAMP_K_MAX 1024
@@ -78,9 +79,25 @@ typedef struct fsamp_plan {
 int fsamp_make_plan(const void* logits, int64_t B, int64_t V, int64_t top_k,
                     int64_t splits_override, fsamp_plan* plan);
 
-/* Bytes of workspace a call with these arguments needs (0 when the plan has one split). */
+/* Bytes of single-buffer workspace a call with these arguments needs: always the counter
+ * regions (round_up(128*B, 256) + 256 bytes), plus B*splits*k*8 candidate bytes when the plan
+ * splits rows.  Returns 0 only for invalid arguments (fsamp_make_plan gives the reason). */
 size_t fsamp_workspace_bytes(const void* logits, int64_t B, int64_t V, int64_t top_k,
                              int64_t splits_override);
+
+/* The two parts of the split workspace that fsamp_run, fsamp_topk_shard take (no counterpart in
+ * the reference, which allocates its per-split partials per call and needs no counters):
+ *   counters  fsamp_counter_bytes(B) bytes of per-row arrival counters.  They must be zero
+ *             before the first call and every call leaves them zero, so one buffer, zeroed once
+ *             (fsamp_workspace_init), serves every later call on a stream; calls that run
+ *             concurrently (different streams) need their own.
+ *   scratch   fsamp_scratch_bytes(...) bytes of per-split candidates, any contents (0 when the
+ *             plan has one split: scratch may then be NULL, and counters too).
+ * Because the counters never share memory with the candidates, calls of any batch size can
+ * share one counter buffer in any order (HIP graphs captured at several sizes included). */
+size_t fsamp_counter_bytes(int64_t B);
+size_t fsamp_scratch_bytes(const void* logits, int64_t B, int64_t V, int64_t top_k,
+                           int64_t splits_override);
 
 /* Zero `bytes` of workspace on `stream` with a fill kernel (graph-capturable). */
 int fsamp_workspace_init(void* ws, size_t bytes, hipStream_t stream);
@@ -112,8 +129,9 @@ int fsamp_sample(const void* logits, int dtype, int64_t B, int64_t V, int64_t to
  *                   it on every replay).  The call's `offset` argument is then ignored.  The
  *                   grid counter in the workspace is used, so ws is required.
  * No counterpart in the reference for the per-row arrays (SEMANTICS.md lists them as open);
- * the counter replaces the graph-capturable generator path of sample_fused with offset < 0
- * (csrc/fused_sampling.cu:112-118, :441-447).
+ * the counter is an in-kernel alternative to the reference's generator path (sample_fused
+ * with offset < 0 takes torch's Philox state, csrc/fused_sampling.cu:441-447), which
+ * fsamp_run's seed_ptr / offset_ptr reproduce exactly.
  */
 typedef struct fsamp_row_params {
   const int32_t* top_k;
@@ -131,6 +149,82 @@ int fsamp_sample_ex(const void* logits, int dtype, int64_t B, int64_t V, int64_t
                     double top_p, const float* u, uint64_t seed, uint64_t offset,
                     const fsamp_row_params* rows, int64_t* out, uint8_t* keep, float* renormed,
                     void* ws, size_t ws_bytes, int64_t splits_override, hipStream_t stream);
+
+/*
+ * One call described in full: every option of the entry points above, with a row stride, the
+ * split workspace, and the seed / offset either as values or as device pointers read in the
+ * kernel.  The torch binding (fused_sampling) calls this.  Output modes, exactly one of:
+ *   out       [B] int64 token ids (keep / renormed [B, k] may be added, as in fsamp_stages);
+ *   ids       [B, k] int64 candidate ids (fsamp_topk);
+ *   words     [B, k] uint64 sorted candidate words (fsamp_topk_shard).
+ * The uniform of row b, when u == NULL, is splitmix64(S, O, b) with
+ *   S = seed_ptr ? *seed_ptr : seed,     O = (offset_ptr ? *offset_ptr : 0) + offset,
+ * which is how the reference unpacks torch's Philox state (at::cuda::philox::unpack for
+ * csrc/fused_sampling.cu:296-300): eager calls pass the generator's (seed, offset) values, a
+ * call captured in a HIP graph passes the graph's seed and offset pointers and its offset
+ * within the graph, so eager calls and graph replays draw from one generator stream.
+ */
+typedef struct fsamp_call {
+  size_t struct_bytes;             /* sizeof(fsamp_call) (FSAMP_ERR_VERSION otherwise) */
+  const void* logits;              /* row b at logits + b*ld elements */
+  int32_t dtype;
+  int32_t threads_override;        /* 0, or force the workgroup size 256/512/1024 (tuning) */
+  int64_t batch, vocab;
+  int64_t ld;                      /* elements between rows; 0 means vocab */
+  int64_t top_k;
+  double top_p;
+  int64_t splits_override;
+  const float* u;                  /* [B] uniforms in [0,1), or NULL */
+  uint64_t seed, offset;
+  const int64_t* seed_ptr;         /* device, or NULL */
+  const int64_t* offset_ptr;       /* device, or NULL */
+  const int32_t* top_k_row;        /* per-row controls as in fsamp_row_params, or NULL */
+  const float* top_p_row;
+  const float* temperature_row;
+  int64_t* out;
+  uint8_t* keep;
+  float* renormed;
+  int64_t* ids;
+  uint64_t* words;
+  int64_t id_offset;               /* words mode: added to every id (0 <= id_offset, and
+                                      id_offset + vocab < 2^32 - 1) */
+  void* counters;                  /* split workspace (fsamp_counter_bytes(batch)) */
+  size_t counter_bytes;
+  void* scratch;                   /* split workspace (fsamp_scratch_bytes(...)) */
+  size_t scratch_bytes;
+} fsamp_call;
+
+int fsamp_run(const fsamp_call* call, hipStream_t stream);
+
+/*
+ * Vocabulary-parallel selection, one shard: logits [B, V_shard] (row stride ld) are columns
+ * [id_offset, id_offset + V_shard) of the whole rows.  Writes the shard's top_k candidates of
+ * every row as words[b*top_k + i] = (key << 32) | (0xFFFFFFFF - (id_offset + id)), sorted
+ * descending (value, then lowest id), the same word the row's split workgroups hand to its
+ * merge.  Needs top_k <= V_shard.  Lifts the reference's per-split contract (unsorted top-K per
+ * split in partial[B, splits, K], csrc/fused_sampling.cu:156, :242) from workgroups to shards;
+ * a tensor-parallel LM head gathers the B x top_k words of every shard (one all-gather) and
+ * calls fsamp_merge_sample on the N lists.  Workspace as fsamp_run.
+ */
+int fsamp_topk_shard(const void* logits, int dtype, int64_t B, int64_t V_shard, int64_t ld,
+                     int64_t top_k, int64_t id_offset, uint64_t* words, void* counters,
+                     size_t counter_bytes, void* scratch, size_t scratch_bytes,
+                     int64_t splits_override, hipStream_t stream);
+
+/*
+ * Merge N sorted candidate lists per row and sample: words [B, N, k] (each list as
+ * fsamp_topk_shard writes it; a short list ends in zero words, and the N lists of a row must
+ * hold at least k candidate words between them) -> the row's top k -> the fp32
+ * tail of fsamp_sample (u, or splitmix64(seed, offset, row) when u == NULL) -> out[B] token
+ * ids (keep / renormed [B, k] optional), or, with out == NULL, ids [B, k] of the merged top k.
+ * dtype says how the keys decode to values.  One wave per row.  Replaces the reference's
+ * merge over splits*K partial candidates (merge_sample_kernel / merge_ids_kernel,
+ * csrc/fused_sampling.cu:245-329) with N shard lists in place of the splits.
+ */
+int fsamp_merge_sample(const uint64_t* words, int dtype, int64_t B, int64_t n_lists, int64_t k,
+                       double top_p, const float* u, uint64_t seed, uint64_t offset,
+                       int64_t* out, uint8_t* keep, float* renormed, int64_t* ids,
+                       hipStream_t stream);
 
 /*
  * Debug form of fsamp_sample that also writes, per row and rank i < k,
@@ -215,11 +309,6 @@ int fsamp_debug_sample_traced(const void* logits, int dtype, int64_t B, int64_t 
                               int64_t top_k, double top_p, const float* u, int64_t* out,
                               void* ws, size_t ws_bytes, int64_t splits_override,
                               int64_t* trace, hipStream_t stream);
-
-/* Tuning aid with no counterpart in the reference: force the workgroup size (256, 512 or
- * 1024) that later plans use, or 0 for the automatic choice.  Process-wide, not thread-safe;
- * a plan that cannot be tiled at that size fails with FSAMP_ERR_VOCAB. */
-int fsamp_debug_force_threads(int32_t threads);
 
 #ifdef __cplusplus
 }

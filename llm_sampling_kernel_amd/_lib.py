@@ -32,6 +32,21 @@ class RowParams(ctypes.Structure):
     _fields_ = [("top_k", _vp), ("top_p", _vp), ("temperature", _vp), ("offset_counter", _vp)]
 
 
+class Call(ctypes.Structure):
+    """fsamp_call (include/fsamp.h), field for field."""
+    _fields_ = [("struct_bytes", _sz), ("logits", _vp), ("dtype", _i32),
+                ("threads_override", _i32), ("batch", _i64), ("vocab", _i64), ("ld", _i64),
+                ("top_k", _i64), ("top_p", _dbl), ("splits_override", _i64), ("u", _vp),
+                ("seed", _u64), ("offset", _u64), ("seed_ptr", _vp), ("offset_ptr", _vp),
+                ("top_k_row", _vp), ("top_p_row", _vp), ("temperature_row", _vp),
+                ("out", _vp), ("keep", _vp), ("renormed", _vp), ("ids", _vp), ("words", _vp),
+                ("id_offset", _i64), ("counters", _vp), ("counter_bytes", _sz),
+                ("scratch", _vp), ("scratch_bytes", _sz)]
+
+    def __init__(self, **kw):
+        super().__init__(struct_bytes=ctypes.sizeof(Call), **kw)
+
+
 class AttrRow(ctypes.Structure):
     _fields_ = [("name", ctypes.c_char * 64), ("threads", _i32), ("chunks", _i32),
                 ("vgprs", _i32), ("scratch_bytes", _i32), ("lds_bytes", _i32),
@@ -57,7 +72,13 @@ SIGNATURES = {
     "fsamp_probe_scan_split": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _sz, _vp]),
     "fsamp_probe_load": (_i32, [_vp, _i32, _i64, _i64, _vp, _vp]),
     "fsamp_kernel_attrs": (_i32, [ctypes.POINTER(AttrRow), _i32, ctypes.POINTER(_i32)]),
-    "fsamp_debug_force_threads": (_i32, [_i32]),
+    "fsamp_counter_bytes": (_sz, [_i64]),
+    "fsamp_scratch_bytes": (_sz, [_vp, _i64, _i64, _i64, _i64]),
+    "fsamp_run": (_i32, [ctypes.c_void_p, _vp]),
+    "fsamp_topk_shard": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _sz, _vp, _sz,
+                                _i64, _vp]),
+    "fsamp_merge_sample": (_i32, [_vp, _i32, _i64, _i64, _i64, _dbl, _vp, _u64, _u64, _vp, _vp,
+                                  _vp, _vp, _vp]),
     "fsamp_debug_wave_selftest": (_i32, [_vp, _vp]),
     "fsamp_debug_sample_traced": (_i32, [_vp, _i32, _i64, _i64, _i64, _dbl, _vp, _vp, _vp, _sz,
                                          _i64, _vp, _vp]),

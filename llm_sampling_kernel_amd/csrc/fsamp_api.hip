@@ -21,10 +21,7 @@ size_t round_up(size_t a, size_t b) { return (a + b - 1) / b * b; }
 
 // per-row arrival counters, one 128-byte line each (atomics on one line serialise)
 size_t counter_bytes(int64_t B) { return round_up((size_t)B * TICKET_STRIDE * 4u, 256); }
-constexpr size_t kGridCounterBytes = 256;  // the grid counter of the graph-safe draw
-
-// Tiling preference forced by fsamp_debug_force_threads (0 = automatic).
-int g_force_threads = 0;
+constexpr size_t kGridCounterBytes = 256;  // the grid counter of the in-kernel offset advance
 
 // Split count when the caller does not force one: one workgroup per row once the batch alone
 // fills half the CUs; below that, splits shorten each workgroup's selection chain (the
@@ -40,11 +37,11 @@ int auto_splits(int64_t B, int64_t V) {
 }
 
 // Workgroup size for a slice: 256 threads while 8 chunks per thread hold it, then 512 (up to
-// 38 chunks, 8 waves with room for the slice in VGPRs), then 1024;
-// never fewer threads than k (the slice's lower bound ranks one maximum per thread and the
-// candidate sort one candidate per thread).
-int preferred_threads(int slice, int K) {
-  int want = g_force_threads > 0 ? g_force_threads
+// 38 chunks, 8 waves with room for the slice in VGPRs), then 1024; `force` (a tuning override)
+// replaces the choice; never fewer threads than k (the slice's lower bound ranks one maximum
+// per thread and the candidate sort one candidate per thread).
+int preferred_threads(int slice, int K, int force) {
+  int want = force > 0 ? force
              : (slice <= 256 * 8 * 8 ? 256 : (slice <= 512 * 8 * 38 ? 512 : 1024));
   while (want < K) want *= 2;
   return want;
@@ -52,8 +49,8 @@ int preferred_threads(int slice, int K) {
 
 // Smallest compiled tiling of the preferred workgroup size that holds `slice` elements; when
 // that size has none large enough, the smallest-capacity tiling of any size (unless forced).
-const KernelEntry* pick_tiling(int slice, int vec, int K) {
-  const int want = preferred_threads(slice, K);
+const KernelEntry* pick_tiling(int slice, int vec, int K, int force) {
+  const int want = preferred_threads(slice, K, force);
   const KernelEntry* best = nullptr;
   const KernelEntry* any = nullptr;
   for (int i = 0; i < kNumKernels; ++i) {
@@ -63,7 +60,7 @@ const KernelEntry* pick_tiling(int slice, int vec, int K) {
     if (e.threads == want && (best == nullptr || e.chunks < best->chunks)) best = &e;
     if (any == nullptr || cap < (int64_t)any->threads * any->chunks * 8) any = &e;
   }
-  if (best != nullptr || g_force_threads > 0) return best;
+  if (best != nullptr || force > 0) return best;
   return any;
 }
 
@@ -75,13 +72,14 @@ int validate(int dtype, int64_t B, int64_t V, int64_t top_k) {
   return FSAMP_OK;
 }
 
-int make_plan_impl(const void* logits, int64_t B, int64_t V, int64_t top_k, int64_t splits_override,
-                   fsamp_plan* pl, const KernelEntry** kern) {
+int make_plan_impl(const void* logits, int64_t B, int64_t V, int64_t ld, int64_t top_k,
+                   int64_t splits_override, int force_threads, fsamp_plan* pl,
+                   const KernelEntry** kern) {
   pl->batch = B;
   pl->vocab = V;
   pl->k = std::min(top_k, V);
   const int K = (int)pl->k;
-  const bool vec = ((uintptr_t)logits % 16 == 0) && (V % 8 == 0);
+  const bool vec = ((uintptr_t)logits % 16 == 0) && (V % 8 == 0) && (ld % 8 == 0);
   const int units = (int)((V + 7) / 8);
   int S = splits_override > 0 ? (int)std::min<int64_t>(splits_override, 1 << 20) : auto_splits(B, V);
   // the row's last workgroup merges S*K words in LDS, ranking across at most MAX_SPLITS lists
@@ -90,7 +88,7 @@ int make_plan_impl(const void* logits, int64_t B, int64_t V, int64_t top_k, int6
   int slice = 0;
   for (;;) {
     slice = ((units + S - 1) / S) * 8;
-    e = pick_tiling(slice, vec ? 1 : 0, K);
+    e = pick_tiling(slice, vec ? 1 : 0, K, force_threads);
     if (e != nullptr) break;
     if (S >= CAND_CAP / K || S >= MAX_SPLITS || S >= units) return FSAMP_ERR_VOCAB;
     ++S;
@@ -108,67 +106,149 @@ int make_plan_impl(const void* logits, int64_t B, int64_t V, int64_t top_k, int6
   return FSAMP_OK;
 }
 
+size_t scratch_bytes_of(const fsamp_plan& pl) {
+  return pl.splits > 1 ? (size_t)pl.batch * (size_t)pl.splits * (size_t)pl.k * 8u : 0u;
+}
+
 __global__ void fill_zero_kernel(uint32_t* p, size_t n) {
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
        i += (size_t)gridDim.x * blockDim.x)
     p[i] = 0u;
 }
 
-int launch(const void* logits, int dtype, int64_t B, int64_t V, int64_t top_k, double top_p,
-           const float* u, uint64_t seed, uint64_t offset, int64_t* out, int64_t* ids,
-           uint8_t* keep, float* renormed, int stop, void* ws, size_t ws_bytes,
-           int64_t splits_override, hipStream_t stream, int64_t* trace = nullptr,
-           const fsamp_row_params* rows = nullptr) {
-  int rc = validate(dtype, B, V, top_k);
+// One sampler launch, whatever entry point it came through.  The workspace arrives in one of
+// two forms: a single buffer `ws` laid out as [tickets][grid counter][partials] (the classic
+// entry points), or separate `counters` (tickets, persistent and zero between calls) and
+// `scratch` (partials, any contents) buffers (fsamp_run and the fixed-scratch entry point).
+struct Call {
+  const void* logits = nullptr;
+  int dtype = FSAMP_DTYPE_BF16;
+  int64_t B = 0, V = 0, ld = 0, top_k = 0;
+  double top_p = 1.0;
+  int64_t splits_override = 0;
+  int force_threads = 0;
+  const float* u = nullptr;
+  uint64_t seed = 0, offset = 0;
+  const uint64_t* seed_src = nullptr;
+  const uint64_t* offset_src = nullptr;
+  uint64_t* offset_ctr = nullptr;  // fsamp_sample_ex's in-kernel counter
+  const int32_t* topk_row = nullptr;
+  const float* topp_row = nullptr;
+  const float* temp_row = nullptr;
+  int64_t* out = nullptr;
+  int64_t* ids = nullptr;
+  uint64_t* words = nullptr;
+  uint32_t id_offset = 0;
+  uint8_t* keep = nullptr;
+  float* renormed = nullptr;
+  int stop = 7;
+  int64_t* trace = nullptr;
+  // workspace, single-buffer form
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+  // workspace, split form
+  bool split_ws = false;
+  void* counters = nullptr;
+  size_t counters_bytes = 0;
+  void* scratch = nullptr;
+  size_t scratch_bytes = 0;
+};
+
+int launch(const Call& c, hipStream_t stream) {
+  int rc = validate(c.dtype, c.B, c.V, c.top_k);
   if (rc != FSAMP_OK) return rc;
-  if (!(top_p > 0.0 && top_p <= 1.0)) return FSAMP_ERR_TOPP;
-  if (logits == nullptr || (out == nullptr && ids == nullptr)) return FSAMP_ERR_NULL;
-  if ((keep == nullptr) != (renormed == nullptr)) return FSAMP_ERR_NULL;
+  if (c.ld < c.V) return FSAMP_ERR_SHAPE;
+  if (!(c.top_p > 0.0 && c.top_p <= 1.0)) return FSAMP_ERR_TOPP;
+  const int modes = (c.out != nullptr) + (c.ids != nullptr) + (c.words != nullptr);
+  if (c.logits == nullptr || modes != 1) return FSAMP_ERR_NULL;
+  if ((c.keep == nullptr) != (c.renormed == nullptr)) return FSAMP_ERR_NULL;
+  if (c.keep != nullptr && c.out == nullptr) return FSAMP_ERR_NULL;
   fsamp_plan pl;
   const KernelEntry* e = nullptr;
-  rc = make_plan_impl(logits, B, V, top_k, splits_override, &pl, &e);
+  rc = make_plan_impl(c.logits, c.B, c.V, c.ld, c.top_k, c.splits_override, c.force_threads, &pl,
+                      &e);
   if (rc != FSAMP_OK) return rc;
-  const bool use_ctr = rows != nullptr && rows->offset_counter != nullptr && u == nullptr;
-  if ((pl.splits > 1 || use_ctr) && (ws == nullptr || ws_bytes < pl.workspace_bytes))
-    return FSAMP_ERR_WORKSPACE;
+  if (c.words != nullptr && (uint64_t)c.id_offset + (uint64_t)c.V > 0xFFFFFFFEull)
+    return FSAMP_ERR_SHAPE;
   Params p;
-  p.logits = static_cast<const uint16_t*>(logits);
-  p.out = out;
-  p.ids = ids;
-  p.keep = keep;
-  p.renormed = renormed;
-  p.u = u;
-  p.seed = seed;
-  p.offset = offset;
-  p.tickets = static_cast<uint32_t*>(ws);
-  p.grid_ticket = ws != nullptr
-                      ? reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + counter_bytes(B))
-                      : nullptr;
-  p.partials = pl.splits > 1 ? reinterpret_cast<uint64_t*>(static_cast<char*>(ws) +
-                                                           counter_bytes(B) + kGridCounterBytes)
-                             : nullptr;
-  p.offset_ctr = use_ctr ? reinterpret_cast<uint64_t*>(rows->offset_counter) : nullptr;
-  p.topk_row = rows != nullptr ? rows->top_k : nullptr;
-  p.topp_row = rows != nullptr ? rows->top_p : nullptr;
-  p.temp_row = rows != nullptr ? rows->temperature : nullptr;
-  p.B = (int)B;
-  p.V = (int)V;
+  memset(&p, 0, sizeof(p));
+  const bool use_ctr = c.offset_ctr != nullptr && c.u == nullptr;
+  if (!c.split_ws) {
+    if ((pl.splits > 1 || use_ctr) && (c.ws == nullptr || c.ws_bytes < pl.workspace_bytes))
+      return FSAMP_ERR_WORKSPACE;
+    char* ws = static_cast<char*>(c.ws);
+    p.tickets = reinterpret_cast<uint32_t*>(ws);
+    p.grid_ticket = ws != nullptr ? reinterpret_cast<uint32_t*>(ws + counter_bytes(c.B)) : nullptr;
+    p.partials = pl.splits > 1
+                     ? reinterpret_cast<uint64_t*>(ws + counter_bytes(c.B) + kGridCounterBytes)
+                     : nullptr;
+  } else {
+    if (use_ctr) return FSAMP_ERR_WORKSPACE;  // the split form has no grid counter
+    if (pl.splits > 1) {
+      if (c.counters == nullptr || c.counters_bytes < counter_bytes(c.B) || c.scratch == nullptr ||
+          c.scratch_bytes < scratch_bytes_of(pl))
+        return FSAMP_ERR_WORKSPACE;
+      p.tickets = static_cast<uint32_t*>(c.counters);
+      p.partials = static_cast<uint64_t*>(c.scratch);
+    }
+  }
+  p.logits = static_cast<const uint16_t*>(c.logits);
+  p.out = c.out;
+  p.ids = c.ids;
+  p.words = c.words;
+  p.id_offset = c.id_offset;
+  p.keep = c.keep;
+  p.renormed = c.renormed;
+  p.u = c.u;
+  p.seed = c.seed;
+  // the in-kernel counter of fsamp_sample_ex supplies the whole offset
+  p.offset = use_ctr ? 0ull : c.offset;
+  p.seed_src = c.u == nullptr ? c.seed_src : nullptr;
+  p.offset_src = c.u == nullptr ? (use_ctr ? c.offset_ctr : c.offset_src) : nullptr;
+  p.offset_ctr = use_ctr ? c.offset_ctr : nullptr;
+  p.topk_row = c.topk_row;
+  p.topp_row = c.topp_row;
+  p.temp_row = c.temp_row;
+  p.B = (int)c.B;
+  p.V = (int)c.V;
+  p.ld = c.ld;
   p.K = (int)pl.k;
   p.S = pl.splits;
   p.slice = pl.slice;
-  p.top_p_f = (float)top_p;
-  p.keep_all = top_p >= 1.0 ? 1 : 0;
-  p.is_bf16 = dtype == FSAMP_DTYPE_BF16 ? 1 : 0;
+  p.top_p_f = (float)c.top_p;
+  p.keep_all = c.top_p >= 1.0 ? 1 : 0;
+  p.is_bf16 = c.dtype == FSAMP_DTYPE_BF16 ? 1 : 0;
   p.vec = pl.vec;
-  p.stop = stop;
-  p.trace = trace;
+  p.stop = c.stop;
+  p.trace = c.trace;
   void* args[] = {&p};
   const void* fn = (pl.k > 128 && pl.splits > 1) ? e->fn_merge : e->fn;
-  const hipError_t err = hipLaunchKernel(fn, dim3((unsigned)(B * pl.splits)), dim3(e->threads),
+  const hipError_t err = hipLaunchKernel(fn, dim3((unsigned)(c.B * pl.splits)), dim3(e->threads),
                                          args, 0, stream);
   if (err != hipSuccess) return FSAMP_ERR_LAUNCH;
   if (hipGetLastError() != hipSuccess) return FSAMP_ERR_LAUNCH;
   return FSAMP_OK;
+}
+
+// The classic argument list as a Call (contiguous rows, single-buffer workspace).
+Call classic(const void* logits, int dtype, int64_t B, int64_t V, int64_t top_k, double top_p,
+             const float* u, uint64_t seed, uint64_t offset, void* ws, size_t ws_bytes,
+             int64_t splits_override) {
+  Call c;
+  c.logits = logits;
+  c.dtype = dtype;
+  c.B = B;
+  c.V = V;
+  c.ld = V;
+  c.top_k = top_k;
+  c.top_p = top_p;
+  c.u = u;
+  c.seed = seed;
+  c.offset = offset;
+  c.ws = ws;
+  c.ws_bytes = ws_bytes;
+  c.splits_override = splits_override;
+  return c;
 }
 
 }  // namespace
@@ -192,6 +272,7 @@ const char* fsamp_error_string(int status) {
     case FSAMP_ERR_SPLITS: return "splits must be >= 1";
     case FSAMP_ERR_VOCAB: return "vocabulary too large for the workgroup tiling";
     case FSAMP_ERR_LAUNCH: return "HIP kernel launch failed";
+    case FSAMP_ERR_VERSION: return "fsamp_call.struct_bytes does not match this library";
     default: return "unknown fsamp status";
   }
 }
@@ -201,7 +282,7 @@ int fsamp_make_plan(const void* logits, int64_t B, int64_t V, int64_t top_k,
   if (plan == nullptr) return FSAMP_ERR_NULL;
   const int rc = validate(FSAMP_DTYPE_BF16, B, V, top_k);
   if (rc != FSAMP_OK) return rc;
-  return make_plan_impl(logits, B, V, top_k, splits_override, plan, nullptr);
+  return make_plan_impl(logits, B, V, V, top_k, splits_override, 0, plan, nullptr);
 }
 
 size_t fsamp_workspace_bytes(const void* logits, int64_t B, int64_t V, int64_t top_k,
@@ -209,6 +290,15 @@ size_t fsamp_workspace_bytes(const void* logits, int64_t B, int64_t V, int64_t t
   fsamp_plan pl;
   if (fsamp_make_plan(logits, B, V, top_k, splits_override, &pl) != FSAMP_OK) return 0;
   return pl.workspace_bytes;
+}
+
+size_t fsamp_counter_bytes(int64_t B) { return B < 1 ? 0 : counter_bytes(B); }
+
+size_t fsamp_scratch_bytes(const void* logits, int64_t B, int64_t V, int64_t top_k,
+                           int64_t splits_override) {
+  fsamp_plan pl;
+  if (fsamp_make_plan(logits, B, V, top_k, splits_override, &pl) != FSAMP_OK) return 0;
+  return scratch_bytes_of(pl);
 }
 
 int fsamp_workspace_init(void* ws, size_t bytes, hipStream_t stream) {
@@ -222,12 +312,53 @@ int fsamp_workspace_init(void* ws, size_t bytes, hipStream_t stream) {
   return hipGetLastError() == hipSuccess ? FSAMP_OK : FSAMP_ERR_LAUNCH;
 }
 
+int fsamp_run(const fsamp_call* a, hipStream_t stream) {
+  if (a == nullptr) return FSAMP_ERR_NULL;
+  if (a->struct_bytes != sizeof(fsamp_call)) return FSAMP_ERR_VERSION;
+  if (a->threads_override != 0 && a->threads_override != 256 && a->threads_override != 512 &&
+      a->threads_override != 1024)
+    return FSAMP_ERR_SHAPE;
+  if (a->id_offset < 0 || a->id_offset > (int64_t)0xFFFFFFFF) return FSAMP_ERR_SHAPE;
+  Call c;
+  c.logits = a->logits;
+  c.dtype = a->dtype;
+  c.B = a->batch;
+  c.V = a->vocab;
+  c.ld = a->ld == 0 ? a->vocab : a->ld;
+  c.top_k = a->top_k;
+  c.top_p = a->top_p;
+  c.splits_override = a->splits_override;
+  c.force_threads = a->threads_override;
+  c.u = a->u;
+  c.seed = a->seed;
+  c.offset = a->offset;
+  c.seed_src = reinterpret_cast<const uint64_t*>(a->seed_ptr);
+  c.offset_src = reinterpret_cast<const uint64_t*>(a->offset_ptr);
+  c.topk_row = a->top_k_row;
+  c.topp_row = a->top_p_row;
+  c.temp_row = a->temperature_row;
+  c.out = a->out;
+  c.ids = a->ids;
+  c.words = a->words;
+  c.id_offset = (uint32_t)a->id_offset;
+  c.keep = a->keep;
+  c.renormed = a->renormed;
+  c.split_ws = true;
+  c.counters = a->counters;
+  c.counters_bytes = a->counter_bytes;
+  c.scratch = a->scratch;
+  c.scratch_bytes = a->scratch_bytes;
+  return launch(c, stream);
+}
+
 int fsamp_sample(const void* logits, int dtype, int64_t B, int64_t V, int64_t top_k,
                  double top_p, const float* u, uint64_t seed, uint64_t offset, int64_t* out,
                  void* ws, size_t ws_bytes, int64_t splits_override, hipStream_t stream) {
   if (out == nullptr) return FSAMP_ERR_NULL;
-  return launch(logits, dtype, B, V, top_k, top_p, u, seed, offset, out, nullptr, nullptr,
-                nullptr, 7, ws, ws_bytes, splits_override, stream);
+  Call c = classic(logits, dtype, B, V, top_k, top_p, u, seed, offset, ws, ws_bytes,
+                   splits_override);
+  c.out = out;
+  return launch(c, stream);
 }
 
 int fsamp_sample_ex(const void* logits, int dtype, int64_t B, int64_t V, int64_t top_k,
@@ -235,8 +366,18 @@ int fsamp_sample_ex(const void* logits, int dtype, int64_t B, int64_t V, int64_t
                     const fsamp_row_params* rows, int64_t* out, uint8_t* keep, float* renormed,
                     void* ws, size_t ws_bytes, int64_t splits_override, hipStream_t stream) {
   if (out == nullptr) return FSAMP_ERR_NULL;
-  return launch(logits, dtype, B, V, top_k, top_p, u, seed, offset, out, nullptr, keep, renormed,
-                7, ws, ws_bytes, splits_override, stream, nullptr, rows);
+  Call c = classic(logits, dtype, B, V, top_k, top_p, u, seed, offset, ws, ws_bytes,
+                   splits_override);
+  c.out = out;
+  c.keep = keep;
+  c.renormed = renormed;
+  if (rows != nullptr) {
+    c.topk_row = rows->top_k;
+    c.topp_row = rows->top_p;
+    c.temp_row = rows->temperature;
+    c.offset_ctr = rows->offset_counter;
+  }
+  return launch(c, stream);
 }
 
 int fsamp_stages(const void* logits, int dtype, int64_t B, int64_t V, int64_t top_k,
@@ -244,16 +385,21 @@ int fsamp_stages(const void* logits, int dtype, int64_t B, int64_t V, int64_t to
                  uint8_t* keep, float* renormed, void* ws, size_t ws_bytes,
                  int64_t splits_override, hipStream_t stream) {
   if (out == nullptr || keep == nullptr || renormed == nullptr) return FSAMP_ERR_NULL;
-  return launch(logits, dtype, B, V, top_k, top_p, u, seed, offset, out, nullptr, keep,
-                renormed, 7, ws, ws_bytes, splits_override, stream);
+  Call c = classic(logits, dtype, B, V, top_k, top_p, u, seed, offset, ws, ws_bytes,
+                   splits_override);
+  c.out = out;
+  c.keep = keep;
+  c.renormed = renormed;
+  return launch(c, stream);
 }
 
 int fsamp_topk(const void* logits, int dtype, int64_t B, int64_t V, int64_t top_k,
                int64_t* ids, void* ws, size_t ws_bytes, int64_t splits_override,
                hipStream_t stream) {
   if (ids == nullptr) return FSAMP_ERR_NULL;
-  return launch(logits, dtype, B, V, top_k, 1.0, nullptr, 0, 0, nullptr, ids, nullptr, nullptr,
-                7, ws, ws_bytes, splits_override, stream);
+  Call c = classic(logits, dtype, B, V, top_k, 1.0, nullptr, 0, 0, ws, ws_bytes, splits_override);
+  c.ids = ids;
+  return launch(c, stream);
 }
 
 int fsamp_probe_phase(const void* logits, int dtype, int64_t B, int64_t V, int64_t top_k,
@@ -261,14 +407,11 @@ int fsamp_probe_phase(const void* logits, int dtype, int64_t B, int64_t V, int64
                       int64_t splits_override, hipStream_t stream) {
   if (phase < 1 || phase > 7) return FSAMP_ERR_PHASE;
   if (out == nullptr) return FSAMP_ERR_NULL;
-  return launch(logits, dtype, B, V, top_k, top_p, nullptr, 0, 0, out, nullptr, nullptr, nullptr,
-                (int)phase, ws, ws_bytes, splits_override, stream);
-}
-
-int fsamp_debug_force_threads(int32_t threads) {
-  if (threads != 0 && threads != 256 && threads != 512 && threads != 1024) return FSAMP_ERR_SHAPE;
-  g_force_threads = threads;
-  return FSAMP_OK;
+  Call c = classic(logits, dtype, B, V, top_k, top_p, nullptr, 0, 0, ws, ws_bytes,
+                   splits_override);
+  c.out = out;
+  c.stop = (int)phase;
+  return launch(c, stream);
 }
 
 int fsamp_debug_sample_traced(const void* logits, int dtype, int64_t B, int64_t V,
@@ -276,8 +419,74 @@ int fsamp_debug_sample_traced(const void* logits, int dtype, int64_t B, int64_t 
                                void* ws, size_t ws_bytes, int64_t splits_override,
                                int64_t* trace, hipStream_t stream) {
   if (out == nullptr || trace == nullptr) return FSAMP_ERR_NULL;
-  return launch(logits, dtype, B, V, top_k, top_p, u, 0, 0, out, nullptr, nullptr, nullptr, 7,
-                ws, ws_bytes, splits_override, stream, trace);
+  Call c = classic(logits, dtype, B, V, top_k, top_p, u, 0, 0, ws, ws_bytes, splits_override);
+  c.out = out;
+  c.trace = trace;
+  return launch(c, stream);
+}
+
+int fsamp_topk_shard(const void* logits, int dtype, int64_t B, int64_t V_shard, int64_t ld,
+                     int64_t top_k, int64_t id_offset, uint64_t* words, void* counters,
+                     size_t counter_bytes, void* scratch, size_t scratch_bytes,
+                     int64_t splits_override, hipStream_t stream) {
+  if (words == nullptr) return FSAMP_ERR_NULL;
+  if (top_k > V_shard && V_shard >= 1) return FSAMP_ERR_TOPK_HIGH;
+  fsamp_call a;
+  memset(&a, 0, sizeof(a));
+  a.struct_bytes = sizeof(a);
+  a.logits = logits;
+  a.dtype = dtype;
+  a.batch = B;
+  a.vocab = V_shard;
+  a.ld = ld;
+  a.top_k = top_k;
+  a.top_p = 1.0;
+  a.splits_override = splits_override;
+  a.words = words;
+  a.id_offset = id_offset;
+  a.counters = counters;
+  a.counter_bytes = counter_bytes;
+  a.scratch = scratch;
+  a.scratch_bytes = scratch_bytes;
+  return fsamp_run(&a, stream);
+}
+
+int fsamp_merge_sample(const uint64_t* words, int dtype, int64_t B, int64_t n_lists, int64_t k,
+                       double top_p, const float* u, uint64_t seed, uint64_t offset,
+                       int64_t* out, uint8_t* keep, float* renormed, int64_t* ids,
+                       hipStream_t stream) {
+  if (dtype != FSAMP_DTYPE_F16 && dtype != FSAMP_DTYPE_BF16) return FSAMP_ERR_DTYPE;
+  if (B < 1 || B > (int64_t)0x7FFFFFFF || n_lists < 1 || n_lists > 4096) return FSAMP_ERR_SHAPE;
+  if (k < 1) return FSAMP_ERR_TOPK_LOW;
+  if (k > FSAMP_K_MAX) return FSAMP_ERR_TOPK_HIGH;
+  if (!(top_p > 0.0 && top_p <= 1.0)) return FSAMP_ERR_TOPP;
+  if (words == nullptr || ((out == nullptr) == (ids == nullptr))) return FSAMP_ERR_NULL;
+  if ((keep == nullptr) != (renormed == nullptr) || (keep != nullptr && out == nullptr))
+    return FSAMP_ERR_NULL;
+  Params p;
+  memset(&p, 0, sizeof(p));
+  p.out = out;
+  p.ids = ids;
+  p.keep = keep;
+  p.renormed = renormed;
+  p.u = u;
+  p.seed = seed;
+  p.offset = offset;
+  p.B = (int)B;
+  p.K = (int)k;
+  p.S = 1;
+  p.top_p_f = (float)top_p;
+  p.keep_all = top_p >= 1.0 ? 1 : 0;
+  p.is_bf16 = dtype == FSAMP_DTYPE_BF16 ? 1 : 0;
+  p.stop = 7;
+  const int rb = k <= 64 ? 0 : k <= 128 ? 1 : k <= 256 ? 2 : k <= 512 ? 3 : 4;
+  int nl = (int)n_lists;
+  const uint64_t* w = words;
+  void* args[] = {&p, &w, &nl};
+  const hipError_t err = hipLaunchKernel(kMergeKernels[rb], dim3((unsigned)B), dim3(64), args, 0,
+                                         stream);
+  if (err != hipSuccess || hipGetLastError() != hipSuccess) return FSAMP_ERR_LAUNCH;
+  return FSAMP_OK;
 }
 
 int fsamp_kernel_attrs(fsamp_attr_row* rows, int32_t max_rows, int32_t* n_rows) {

@@ -19,16 +19,21 @@ struct Params {
   int64_t* ids;            // [B, K] candidate ids (topk mode) or nullptr
   uint8_t* keep;           // [B, K] or nullptr
   float* renormed;         // [B, K] or nullptr
+  uint64_t* words;         // [B, K] sorted (key, ~(id_offset + id)) words (shard mode) or nullptr
   const float* u;          // [B] uniforms or nullptr (splitmix64 of seed/offset/row)
   uint64_t seed, offset;
+  const uint64_t* seed_src;    // device seed read in the kernel (replaces seed) or nullptr
+  const uint64_t* offset_src;  // device base offset read in the kernel (offset is added) or nullptr
   uint64_t* partials;      // workspace: [B, S, K] per-split candidates
   uint32_t* tickets;       // workspace: [B] arrival counters, zero between calls
   uint32_t* grid_ticket;   // workspace: rows that have drawn from *offset_ctr, zero between calls
-  uint64_t* offset_ctr;    // graph-safe draw offset (device) or nullptr
+  uint64_t* offset_ctr;    // graph-safe draw offset advanced in the kernel (device) or nullptr
   const int32_t* topk_row; // per-row k, top_p, temperature (device) or nullptr
   const float* topp_row;
   const float* temp_row;
   int B, V, K, S;
+  int64_t ld;              // elements between consecutive rows (>= V)
+  uint32_t id_offset;      // added to every id written to words[]
   int slice;               // elements per split, a multiple of 8
   float top_p_f;           // (float)top_p
   int keep_all;            // top_p >= 1: keep every rank
@@ -66,5 +71,7 @@ struct KernelEntry {
 
 extern const KernelEntry kKernels[];
 extern const int kNumKernels;
+// fsamp_merge_kernel<RB> for RB = 1, 2, 4, 8, 16
+extern const void* const kMergeKernels[5];
 
 }  // namespace fsamp

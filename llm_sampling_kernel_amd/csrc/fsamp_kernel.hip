@@ -88,6 +88,12 @@ __device__ __forceinline__ uint32_t unpack_id(uint64_t w) {
   return 0xFFFFFFFFu - (uint32_t)(w & 0xFFFFFFFFull);
 }
 
+// A candidate word with its id moved by `off` (a shard's first column in the whole row): the
+// low half is ~id, so ~(id + off) = ~id - off.  Zero words (padding past the slice) stay zero.
+__device__ __forceinline__ uint64_t global_word(uint64_t w, uint32_t off) {
+  return w == 0ull ? 0ull : w - (uint64_t)off;
+}
+
 // key -> fp32 value (the exact bf16/fp16 value; the -0 key decodes to +0)
 __device__ __forceinline__ float key_to_float(uint32_t key, int is_bf16) {
   const uint32_t b = (key & 0x8000u) ? (key & 0x7FFFu) : ((0x10000u - key) & 0xFFFFu);
@@ -654,6 +660,14 @@ __device__ __forceinline__ void wave_finish(const Params& p, uint64_t (&v)[RB], 
     }
     return;
   }
+  if (p.words != nullptr) {
+#pragma unroll
+    for (int i = 0; i < RB; ++i) {
+      const int e = l * RB + i;
+      if (e < K) p.words[(size_t)row * K + e] = global_word(v[i], p.id_offset);
+    }
+    return;
+  }
   advance_offset(p);
   const int R = (rc.k + 63) >> 6;
   if (R != RB) {
@@ -958,6 +972,11 @@ __device__ __forceinline__ void wave_back_wide(const Params& p, Smem<NT>& sm, in
     for (int i = l; i < p.K; i += 64) p.ids[(size_t)row * p.K + i] = (int64_t)unpack_id(sm.top[i]);
     return;
   }
+  if (p.words != nullptr) {
+    for (int i = l; i < p.K; i += 64)
+      p.words[(size_t)row * p.K + i] = global_word(sm.top[i], p.id_offset);
+    return;
+  }
   advance_offset(p);
   const uint64_t none[RB] = {};
   sample_tail<RB, true>(p, none, sm.top, rc, row);
@@ -1010,7 +1029,7 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
   const int wid = __builtin_amdgcn_readfirstlane(t >> 6);  // wave-uniform, known to the compiler
   const int row = blockIdx.x / p.S;
   const int split = blockIdx.x - row * p.S;
-  const uint16_t* xr = p.logits + (size_t)row * (size_t)p.V;
+  const uint16_t* xr = p.logits + (size_t)row * (size_t)p.ld;
   const int lo = split * p.slice;
   const int hi = min(lo + p.slice, p.V);
   const int count = max(hi - lo, 0);
@@ -1027,8 +1046,9 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
   const int vz = opaque_vzero();
   const uint64_t* zw = g_zero_words;
   const float u_ld = (p.u != nullptr ? p.u + row : reinterpret_cast<const float*>(zw))[vz];
-  const uint64_t off_ld = __hip_atomic_load((p.offset_ctr != nullptr ? p.offset_ctr : zw) + vz,
+  const uint64_t off_ld = __hip_atomic_load((p.offset_src != nullptr ? p.offset_src : zw) + vz,
                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint64_t seed_ld = (p.seed_src != nullptr ? p.seed_src : zw)[vz];
   const int32_t topk_ld =
       (p.topk_row != nullptr ? p.topk_row + row : reinterpret_cast<const int32_t*>(zw))[vz];
   const float topp_ld =
@@ -1039,14 +1059,18 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
     // (made opaque here, so that no arithmetic on them is hoisted next to their loads)
     float u_v = u_ld, topp_v = topp_ld, temp_v = temp_ld;
     int32_t topk_v = topk_ld;
-    uint64_t off_v = off_ld;
-    asm volatile("" : "+v"(u_v), "+v"(topp_v), "+v"(temp_v), "+v"(topk_v), "+v"(off_v));
+    uint64_t off_v = off_ld, seed_v = seed_ld;
+    asm volatile("" : "+v"(u_v), "+v"(topp_v), "+v"(temp_v), "+v"(topk_v), "+v"(off_v),
+                 "+v"(seed_v));
     RowCtl rc;
     if (p.u != nullptr) {
       rc.u = u_v;
     } else {
-      const uint64_t off = p.offset_ctr != nullptr ? off_v : p.offset;
-      rc.u = rng_uniform(p.seed, off, (uint32_t)row);
+      // the (seed, offset) pair as at::cuda::philox::unpack gives it: device values when the
+      // sources are set (a captured graph's seed and base offset), plus the call's offset
+      const uint64_t seed = p.seed_src != nullptr ? seed_v : p.seed;
+      const uint64_t off = (p.offset_src != nullptr ? off_v : 0ull) + p.offset;
+      rc.u = rng_uniform(seed, off, (uint32_t)row);
     }
     rc.k = p.K;
     rc.top_p = p.top_p_f;
@@ -1544,11 +1568,95 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
   else back(IC<16>{});
 }
 
+// ---- merge of N sorted candidate lists per row (fsamp_merge_sample) ----------------------------
+
+// One wave per row: words[row] holds n_lists descending lists of p.K words (zero words past a
+// short list).  The lists pass through LDS in batches of CAND_CAP / K (at least 4): each batch
+// is staged with every load of it in flight, then folded into the running top K in registers
+// with the bitonic top-merges of the split hand-off.  Every read of a list is an LDS read of
+// the __shared__ array itself, never through a pointer that may address either LDS or global
+// memory (such a pointer compiles to FLAT accesses, whose folded immediate offsets can leave
+// the base address outside the LDS aperture).  The row finishes like the sampler's own: ids of
+// the merged top K, or the fp32 tail.  RB = ceil(K / 64) rounded up to 1, 2, 4, 8 or 16.
+template <int RB>
+__global__ __launch_bounds__(64) void fsamp_merge_kernel(Params p, const uint64_t* words,
+                                                         int n_lists) {
+  __shared__ uint64_t lists[CAND_CAP];
+  __shared__ uint64_t top[FSAMP_K_MAX];
+  const int row = blockIdx.x;
+  const int l = lane_id();
+  const int K = p.K;
+  const uint64_t* src = words + (size_t)row * (size_t)n_lists * (size_t)K;
+  RowCtl rc;
+  rc.u = p.u != nullptr ? p.u[row] : rng_uniform(p.seed, p.offset, (uint32_t)row);
+  rc.k = K;
+  rc.top_p = p.top_p_f;
+  rc.keep_all = p.keep_all;
+  rc.inv_t = 1.0f;
+  const int per = CAND_CAP / K;  // lists per LDS batch
+  uint64_t a[RB], b[RB];
+  for (int s0 = 0; s0 < n_lists; s0 += per) {
+    const int nb = min(per, n_lists - s0);
+    const int n = nb * K;
+    const uint64_t* bsrc = src + (size_t)s0 * (size_t)K;
+    // the previous batch has been read (into registers) before it is overwritten
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    for (int i0 = 0; i0 < n; i0 += 8 * 64) {
+      uint64_t w[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int i = i0 + q * 64 + l;
+        w[q] = i < n ? bsrc[i] : 0ull;
+      }
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int i = i0 + q * 64 + l;
+        if (i < n) lists[i] = w[q];
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    int s = 0;
+    if (s0 == 0) {
+#pragma unroll
+      for (int i = 0; i < RB; ++i) {
+        const int f = l * RB + i;
+        a[i] = f < K ? lists[f] : 0ull;
+      }
+      s = 1;
+    }
+    for (; s < nb; ++s) {
+#pragma unroll
+      for (int i = 0; i < RB; ++i) {
+        const int e = 64 * RB - 1 - (l * RB + i);
+        b[i] = e < K ? lists[s * K + e] : 0ull;
+      }
+      wave_merge_top<RB>(a, b);
+    }
+  }
+  if constexpr (RB <= 4) {
+    wave_finish<RB>(p, a, top, row, rc);
+  } else {
+#pragma unroll
+    for (int i = 0; i < RB; ++i) {
+      const int e = l * RB + i;
+      if (e < K) top[e] = a[i];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    if (p.ids != nullptr) {
+      for (int i = l; i < K; i += 64) p.ids[(size_t)row * K + i] = (int64_t)unpack_id(top[i]);
+      return;
+    }
+    const uint64_t none[RB] = {};
+    sample_tail<RB, true>(p, none, top, rc, row);
+  }
+}
+
 // ---- instantiation table -----------------------------------------------------------------------
 //
 // The instantiations are compiled in eight parts, in parallel: this file built with
-// -DFSAMP_PART=n (n = 0..7) instantiates one group of tilings, common (n even) or MERGE (n odd),
-// and the build without FSAMP_PART holds only the host-side table, which takes the addresses of
+// -DFSAMP_PART=n (n = 0..7) instantiates one group of tilings, common (n even) or MERGE (n odd;
+// part 7 also holds the list-merge kernels), and the build without FSAMP_PART holds only the
+// host-side table, which takes the addresses of
 // every instantiation (their host stubs come from the parts at link time).
 
 #define FSAMP_COMMON_VEC(NT_, CH_) template __global__ void fsamp_kernel<NT_, CH_, true, false>(Params);
@@ -1576,6 +1684,11 @@ FSAMP_KERNEL_LIST_VEC_1024(FSAMP_MERGE_VEC)
 FSAMP_KERNEL_LIST_SCALAR(FSAMP_COMMON_SCALAR)
 #elif FSAMP_PART == 7
 FSAMP_KERNEL_LIST_SCALAR(FSAMP_MERGE_SCALAR)
+template __global__ void fsamp_merge_kernel<1>(Params, const uint64_t*, int);
+template __global__ void fsamp_merge_kernel<2>(Params, const uint64_t*, int);
+template __global__ void fsamp_merge_kernel<4>(Params, const uint64_t*, int);
+template __global__ void fsamp_merge_kernel<8>(Params, const uint64_t*, int);
+template __global__ void fsamp_merge_kernel<16>(Params, const uint64_t*, int);
 #else
 #error "FSAMP_PART must be in [0, 7]"
 #endif
@@ -1603,6 +1716,18 @@ FSAMP_KERNEL_LIST_SCALAR(FSAMP_EXTERN_MERGE_SCALAR)
 const KernelEntry kKernels[] = {FSAMP_KERNEL_LIST_VEC(FSAMP_INST_VEC)
                                     FSAMP_KERNEL_LIST_SCALAR(FSAMP_INST_SCALAR)};
 const int kNumKernels = (int)(sizeof(kKernels) / sizeof(kKernels[0]));
+#endif
+
+extern template __global__ void fsamp_merge_kernel<1>(Params, const uint64_t*, int);
+extern template __global__ void fsamp_merge_kernel<2>(Params, const uint64_t*, int);
+extern template __global__ void fsamp_merge_kernel<4>(Params, const uint64_t*, int);
+extern template __global__ void fsamp_merge_kernel<8>(Params, const uint64_t*, int);
+extern template __global__ void fsamp_merge_kernel<16>(Params, const uint64_t*, int);
+#ifndef __HIP_DEVICE_COMPILE__
+const void* const kMergeKernels[5] = {
+    (const void*)fsamp_merge_kernel<1>, (const void*)fsamp_merge_kernel<2>,
+    (const void*)fsamp_merge_kernel<4>, (const void*)fsamp_merge_kernel<8>,
+    (const void*)fsamp_merge_kernel<16>};
 #endif
 
 #endif  // FSAMP_PART

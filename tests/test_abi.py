@@ -90,3 +90,68 @@ def test_argument_checks_return_the_reference_messages():
                                  ctypes.c_void_p(4096), None, 0, 0, null) == 8
     assert lib.fsamp_probe_scan_split(ctypes.c_void_p(4096), 1, 1, 100, 0,
                                       ctypes.c_void_p(4096), None, 0, null) == 9
+
+
+def test_split_workspace_sizes_and_the_call_struct_checks():
+    lib = _lib.load()
+    assert lib.fsamp_counter_bytes(1) == 256 and lib.fsamp_counter_bytes(3) == 512
+    assert lib.fsamp_counter_bytes(0) == 0
+    p = ctypes.c_void_p(4096)
+    assert lib.fsamp_scratch_bytes(p, 256, 151936, 50, 0) == 0  # one split per row
+    assert lib.fsamp_scratch_bytes(p, 1, 151936, 50, 0) == 6 * 50 * 8
+    assert lib.fsamp_scratch_bytes(p, 16, 151936, 1024, 0) == 16 * 4 * 1024 * 8
+    # a struct of another size is refused before anything else is read
+    c = _lib.Call(logits=4096, dtype=1, batch=1, vocab=100, top_k=5, top_p=0.9, out=4096)
+    c.struct_bytes = ctypes.sizeof(_lib.Call) - 8
+    assert lib.fsamp_run(ctypes.byref(c), None) == 12
+    assert lib.fsamp_error_string(12).startswith(b"fsamp_call")
+    c = _lib.Call(logits=4096, dtype=1, batch=1, vocab=100, top_k=5, top_p=0.9)
+    assert lib.fsamp_run(ctypes.byref(c), None) == 7  # no output
+    c.out, c.ids = 4096, 4096
+    assert lib.fsamp_run(ctypes.byref(c), None) == 7  # two outputs
+    c = _lib.Call(logits=4096, dtype=1, batch=1, vocab=100, ld=50, top_k=5, top_p=0.9, out=4096)
+    assert lib.fsamp_run(ctypes.byref(c), None) == 2  # row stride below the row
+    c = _lib.Call(logits=4096, dtype=1, batch=1, vocab=151936, top_k=50, top_p=0.9, out=4096)
+    assert lib.fsamp_run(ctypes.byref(c), None) == 6  # split rows need counters and scratch
+    c = _lib.Call(logits=4096, dtype=1, batch=1, vocab=100, top_k=5, top_p=0.9, out=4096,
+                  threads_override=384)
+    assert lib.fsamp_run(ctypes.byref(c), None) == 2
+
+
+def test_shard_and_merge_entries_check_their_arguments():
+    lib = _lib.load()
+    p = ctypes.c_void_p(4096)
+    # top_k larger than the shard
+    assert lib.fsamp_topk_shard(p, 1, 2, 64, 64, 65, 0, p, None, 0, None, 0, 0, None) == 4
+    # global ids past 2^32 - 2
+    assert lib.fsamp_topk_shard(p, 1, 2, 64, 64, 8, 0xFFFFFFF0, p, None, 0, None, 0, 0,
+                                None) == 2
+    assert lib.fsamp_merge_sample(p, 3, 2, 4, 8, 0.9, None, 0, 0, p, None, None, None,
+                                  None) == 1
+    assert lib.fsamp_merge_sample(p, 1, 2, 4, 0, 0.9, None, 0, 0, p, None, None, None,
+                                  None) == 3
+    assert lib.fsamp_merge_sample(p, 1, 2, 4, 2000, 0.9, None, 0, 0, p, None, None, None,
+                                  None) == 4
+    assert lib.fsamp_merge_sample(p, 1, 2, 4, 8, 1.5, None, 0, 0, p, None, None, None,
+                                  None) == 5
+    # exactly one of out / ids
+    assert lib.fsamp_merge_sample(p, 1, 2, 4, 8, 0.9, None, 0, 0, p, None, None, p,
+                                  None) == 7
+    assert lib.fsamp_merge_sample(p, 1, 2, 4, 8, 0.9, None, 0, 0, None, None, None, None,
+                                  None) == 7
+
+
+def test_the_torch_module_is_the_compiled_extension_with_the_reference_surface():
+    torch = pytest.importorskip("torch")
+    from llm_sampling_kernel_amd import _fsamp_torch, fused_sampling
+
+    assert os.path.dirname(os.path.abspath(_fsamp_torch.__file__)) == \
+        os.path.dirname(os.path.abspath(_lib.__file__))
+    for name in ("sample_fused", "topk_fused", "stages_fused", "probe_phase", "probe_noop",
+                 "probe_scan_rowblock", "probe_scan_split", "kernel_attrs"):
+        assert getattr(fused_sampling, name) is getattr(_fsamp_torch, name)
+    x = torch.zeros(2, 64, dtype=torch.bfloat16)  # a CPU tensor: refused before any launch
+    with pytest.raises(RuntimeError, match="contiguous cuda"):
+        fused_sampling.sample_fused(x, 5, 0.9, 0, 0, 0)
+    with pytest.raises(RuntimeError, match="contiguous cuda"):
+        fused_sampling.topk_fused(x, 5, 0)

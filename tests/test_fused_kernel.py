@@ -18,6 +18,8 @@ from llm_sampling_kernel_amd import _lib, fused, fused_sampling  # noqa: E402
 from llm_sampling_kernel_amd import workloads as W  # noqa: E402
 from oracle import oracle as O  # noqa: E402
 
+import cabi  # noqa: E402
+
 pytestmark = pytest.mark.gpu
 
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -207,20 +209,18 @@ def test_every_split_count_and_workgroup_size_gives_the_same_answer():
     x = dev(bits, "bfloat16")
     u = ustream(4, 46)
     want = oracle(bits, "bfloat16", 50, 0.9, u)
-    lib = _lib.load()
-    try:
-        for threads in (0, 256, 512, 1024):
-            _lib.check(lib.fsamp_debug_force_threads(threads))
-            for s in (1, 2, 5, 8, 19, 32, 81):
-                try:
-                    tok, ids, keep, ren = run_u(x, 50, 0.9, u, s)
-                except _lib.FsampError as e:
-                    assert e.status == 10  # this size cannot tile the slice: a clean refusal
-                    continue
-                assert np.array_equal(tok, want.token_ids), (threads, s)
-                assert np.array_equal(ren.view(np.uint32), want.renormed.view(np.uint32))
-    finally:
-        lib.fsamp_debug_force_threads(0)
+    ud = torch.from_numpy(u).cuda()
+    for threads in (0, 256, 512, 1024):
+        for s in (1, 2, 5, 8, 19, 32, 81):
+            try:
+                tok, keep, ren = cabi.run(x, 50, 0.9, u=ud, splits=s, threads=threads,
+                                          stages=True)
+            except _lib.FsampError as e:
+                assert e.status == 10  # this size cannot tile the slice: a clean refusal
+                continue
+            assert np.array_equal(tok.cpu().numpy(), want.token_ids), (threads, s)
+            assert np.array_equal(ren.cpu().numpy().view(np.uint32),
+                                  want.renormed.view(np.uint32))
 
 
 # --- sampling (reference :48-108) ---------------------------------------------------------------
@@ -597,12 +597,27 @@ def _uniforms(seed, offset, B):
     return O.rng_uniform(seed, offset, B)
 
 
-def test_generator_draw_under_graph_capture_advances_on_every_replay():
+def test_eager_calls_and_graph_replays_draw_from_one_generator_stream():
+    # The reference takes philox_cuda_state(4) from torch's default generator for every call,
+    # eager or captured (csrc/fused_sampling.cu:441-447), and its test asserts that replays
+    # advance the stream (tests/test_fused_kernel.py:273-285).  Here every eager call and every
+    # replay must draw the uniforms splitmix64(seed, o, row) at the generator offset o it found,
+    # and no two draws -- eager or replayed -- may share an offset.
     B = 16
     bits = randn_bits((B, 6000), 7400, 1.0, "bfloat16")  # flat enough that draws differ
     x = dev(bits, "bfloat16")
+    gen = torch.cuda.default_generators[torch.cuda.current_device()]
     torch.manual_seed(2024)
-    fused.sample_fused(x, 50, 0.95)  # warm-up outside capture creates the device counter
+    seed = gen.initial_seed()
+    used = []
+
+    def eager():
+        o = gen.get_offset()
+        tok = fused.sample_fused(x, 50, 0.95).cpu().numpy()
+        assert gen.get_offset() == o + 4
+        used.append(("eager", o, tok))
+
+    eager()
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -610,25 +625,72 @@ def test_generator_draw_under_graph_capture_advances_on_every_replay():
             fused.sample_fused(x, 50, 0.95)
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
+    used.append(("warm-up", gen.get_offset() - 8, None))
+    used.append(("warm-up", gen.get_offset() - 4, None))
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         out = fused.sample_fused(x, 50, 0.95)
-    ctr = fused_sampling.offset_counter(x.device)
-    seed = torch.cuda.default_generators[0].initial_seed()
-    outs = []
-    for i in range(4):
-        c0 = int(ctr.item())
+    for _ in range(4):
+        eager()
+        o = gen.get_offset()
         g.replay()
         torch.cuda.synchronize()
-        assert int(ctr.item()) == c0 + 4, "each replay advances the counter by 4"
-        want = oracle(bits, "bfloat16", 50, 0.95, _uniforms(seed, c0, B)).token_ids
-        got = out.cpu().numpy()
-        assert np.array_equal(got, want)
-        outs.append(got)
-        fused.sample_fused(x, 50, 0.95)  # eager work between replays uses the host generator
+        assert gen.get_offset() == o + 4, "a replay advances the generator by its 4"
+        used.append(("replay", o, out.cpu().numpy()))
+    eager()
+    offsets = [o for _, o, _ in used]
+    assert len(set(offsets)) == len(offsets), f"two draws shared an offset: {offsets}"
+    for kind, o, tok in used:
+        if tok is None:
+            continue
+        want = oracle(bits, "bfloat16", 50, 0.95, O.rng_uniform(seed, o, B)).token_ids
+        assert np.array_equal(tok, want), (kind, o)
+    replays = [t.tobytes() for k, _, t in used if k == "replay"]
+    assert len(set(replays)) > 1, "replays draw fresh uniforms"
+
+
+def test_graphs_captured_at_several_batch_sizes_replay_in_any_order():
+    # graphs of split-row calls (splits forced) captured at B = 32, 8, 1 on the default capture
+    # stream share the row counters; replaying them in another order must leave every one
+    # correct (the per-call candidates never overlap the counters)
+    V = 20000
+    bits = randn_bits((32, V), 7600, 3.0, "bfloat16")
+    x = dev(bits, "bfloat16")
+    un = ustream(32, 7601)
+    u = torch.from_numpy(un).cuda()
+    want = {B: oracle(bits[:B], "bfloat16", 50, 0.9, un[:B]).token_ids for B in (32, 8, 1)}
+    for B in (32, 8, 1):
+        fused.sample_fused_u(x[:B], 50, 0.9, u[:B], 4)  # warm-up outside capture
+    torch.cuda.synchronize()
+    graphs, outs = {}, {}
+    for B in (32, 8, 1):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            outs[B] = fused.sample_fused_u(x[:B], 50, 0.9, u[:B], 4)
+        graphs[B] = g
+    for B in (1, 8, 32, 8, 1, 1, 32):
+        graphs[B].replay()
         torch.cuda.synchronize()
-        assert int(ctr.item()) == c0 + 4
-    assert len({o.tobytes() for o in outs}) > 1, "replays draw fresh uniforms"
+        assert np.array_equal(outs[B].cpu().numpy(), want[B]), B
+        # eager calls of other sizes in between use the same counters
+        e = fused.sample_fused_u(x[:3], 50, 0.9, u[:3], 4).cpu().numpy()
+        assert np.array_equal(e, oracle(bits[:3], "bfloat16", 50, 0.9, un[:3]).token_ids)
+
+
+def test_device_seed_and_offset_sources_follow_philox_unpack():
+    # fsamp_run with seed_ptr / offset_ptr draws splitmix64(*seed_ptr, *offset_ptr + offset, b)
+    B = 8
+    bits = randn_bits((B, 9000), 7700, 1.0, "bfloat16")
+    x = dev(bits, "bfloat16")
+    sp = torch.tensor([987654321], dtype=torch.int64, device="cuda")
+    op = torch.tensor([4000], dtype=torch.int64, device="cuda")
+    for splits in (1, 3):
+        got = cabi.run(x, 50, 0.95, seed=1, offset=12, seed_ptr=sp, offset_ptr=op, splits=splits)
+        want = oracle(bits, "bfloat16", 50, 0.95, O.rng_uniform(987654321, 4012, B)).token_ids
+        assert np.array_equal(got.cpu().numpy(), want)
+        only_off = cabi.run(x, 50, 0.95, seed=55, offset=3, offset_ptr=op, splits=splits)
+        want = oracle(bits, "bfloat16", 50, 0.95, O.rng_uniform(55, 4003, B)).token_ids
+        assert np.array_equal(only_off.cpu().numpy(), want)
 
 
 def test_the_device_offset_counter_of_the_c_entry_advances_once_per_call():
@@ -643,12 +705,13 @@ def test_the_device_offset_counter_of_the_c_entry_advances_once_per_call():
         for call in range(2):
             c0 = int(ctr.item())
             out = torch.empty(B, dtype=torch.int64, device="cuda")
-            stream = fused_sampling._stream_ptr(x.device)
-            ws, wsb = fused_sampling._ws_args(x, 50, splits, stream)
+            stream = cabi.stream_ptr()
+            ws = cabi.classic_workspace(x, 50, splits)
             _lib.check(lib.fsamp_sample_ex(ctypes.c_void_p(x.data_ptr()), 1, B, V, 50, 0.9, None,
                                            77, 123456, ctypes.byref(rows),
-                                           ctypes.c_void_p(out.data_ptr()), None, None, ws, wsb,
-                                           splits, ctypes.c_void_p(stream)))
+                                           ctypes.c_void_p(out.data_ptr()), None, None,
+                                           cabi.vp(ws), ws.numel(), splits,
+                                           ctypes.c_void_p(stream)))
             torch.cuda.synchronize()
             assert int(ctr.item()) == c0 + 4
             want = oracle(bits, "bfloat16", 50, 0.9, _uniforms(77, c0, B)).token_ids
@@ -657,3 +720,78 @@ def test_the_device_offset_counter_of_the_c_entry_advances_once_per_call():
     assert lib.fsamp_sample_ex(ctypes.c_void_p(x.data_ptr()), 1, B, V, 50, 0.9, None, 77, 0,
                                ctypes.byref(rows), ctypes.c_void_p(out.data_ptr()), None, None,
                                None, 0, 1, None) == 6
+
+
+# --- vocabulary shards: per-shard candidate words, then the merge and draw ---------------------
+
+def _shard_words(x, k, bounds):
+    ws = [fused_sampling.topk_shard(x[:, lo:hi], k, lo) for lo, hi in bounds]
+    return torch.stack(ws, dim=1).contiguous()  # [B, N, k]
+
+
+def _check_shard_words(words, bits, dtype, k, bounds):
+    w = words.cpu().numpy().view(np.uint64)
+    keys = O.key16(bits)
+    for n, (lo, hi) in enumerate(bounds):
+        ids = (0xFFFFFFFF - (w[:, n] & 0xFFFFFFFF)).astype(np.int64)
+        want = oracle(np.ascontiguousarray(bits[:, lo:hi]), dtype, k, 1.0,
+                      np.zeros(bits.shape[0], np.float32)).topk_ids + lo
+        assert np.array_equal(ids, want), n
+        assert np.array_equal((w[:, n] >> 32).astype(np.uint32),
+                              np.take_along_axis(keys, ids, axis=1)), n
+
+
+@pytest.mark.parametrize("name", ["C1", "C5"])
+def test_eight_vocabulary_shards_merge_to_the_whole_row(name):
+    c = W.case(name)
+    x = dev(c.logits, c.dtype)
+    N = 8
+    Vs = c.vocab // N
+    bounds = [(i * Vs, (i + 1) * Vs) for i in range(N)]
+    words = _shard_words(x, c.top_k, bounds)
+    _check_shard_words(words, c.logits, c.dtype, c.top_k, bounds)
+    code = _lib.DTYPE_BF16 if c.dtype == "bfloat16" else _lib.DTYPE_F16
+    ids = fused_sampling.merge_sample(words, code, c.top_p, ids_only=True).cpu().numpy()
+    assert np.array_equal(ids, FIX[f"{name}/topk_ids"])
+    u = torch.from_numpy(c.u).cuda()
+    tok, keep, ren = fused_sampling.merge_sample(words, code, c.top_p, u, stages=True)
+    want = oracle(c.logits, c.dtype, c.top_k, c.top_p, c.u)
+    assert np.array_equal(tok.cpu().numpy(), FIX[f"{name}/token_ids"])
+    assert np.array_equal(keep.cpu().numpy(), want.keep)
+    assert np.array_equal(ren.cpu().numpy().view(np.uint32), want.renormed.view(np.uint32))
+    alone = fused_sampling.merge_sample(words, code, c.top_p, u).cpu().numpy()
+    assert np.array_equal(alone, FIX[f"{name}/token_ids"])
+
+
+@pytest.mark.parametrize("k", [1, 50, 300, 1024])
+def test_uneven_shards_and_wide_merges(k):
+    # unaligned shard widths and offsets take the element-load path; k = 1024 over 8 shards
+    # (8192 words) folds the lists from global memory instead of LDS
+    B, V = 4, 151936 if k == 1024 else 40001
+    bits = randn_bits((B, V), 7800 + k, 2.0, "float16")
+    x = dev(bits, "float16")
+    cuts = [0, 4999, 10007, 20001, 26003, 30000, 33333, 36667, V] if k <= 300 else \
+        [i * (V // 8) for i in range(8)] + [V]
+    bounds = list(zip(cuts[:-1], cuts[1:]))
+    words = _shard_words(x, k, bounds)
+    _check_shard_words(words, bits, "float16", k, bounds)
+    un = ustream(B, 7900 + k)
+    want = oracle(bits, "float16", k, 0.9, un)
+    ids = fused_sampling.merge_sample(words, _lib.DTYPE_F16, 0.9, ids_only=True).cpu().numpy()
+    assert np.array_equal(ids, want.topk_ids)
+    tok = fused_sampling.merge_sample(words, _lib.DTYPE_F16, 0.9, torch.from_numpy(un).cuda())
+    assert np.array_equal(tok.cpu().numpy(), want.token_ids)
+    seeded = fused_sampling.merge_sample(words, _lib.DTYPE_F16, 0.9, seed=5, offset=9)
+    want_s = oracle(bits, "float16", k, 0.9, O.rng_uniform(5, 9, B)).token_ids
+    assert np.array_equal(seeded.cpu().numpy(), want_s)
+
+
+def test_shard_and_merge_argument_checks():
+    x = torch.zeros(2, 64, device="cuda", dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="top_k must be <="):
+        fused_sampling.topk_shard(x, 65, 0)
+    w = torch.zeros(2, 3, 4, dtype=torch.int64, device="cuda")
+    with pytest.raises(RuntimeError, match="top_p must be in"):
+        fused_sampling.merge_sample(w, _lib.DTYPE_BF16, 0.0)
+    with pytest.raises(RuntimeError, match="contiguous int64"):
+        fused_sampling.merge_sample(w.float(), _lib.DTYPE_BF16, 0.5)
