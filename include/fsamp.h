@@ -53,7 +53,8 @@ enum fsamp_status {
   FSAMP_ERR_SPLITS = 9,     /* "splits must be >= 1" (probe) */
   FSAMP_ERR_VOCAB = 10,     /* vocabulary does not fit the workgroup tiling */
   FSAMP_ERR_LAUNCH = 11,    /* the HIP runtime reported an error at launch */
-  FSAMP_ERR_VERSION = 12    /* fsamp_call.struct_bytes is not sizeof(fsamp_call) */
+  FSAMP_ERR_VERSION = 12,   /* fsamp_call.struct_bytes is not sizeof(fsamp_call) */
+  FSAMP_ERR_SCRATCH = 13    /* the call needs more than fsamp_sample_noalloc's fixed scratch */
 };
 
 #define FSAMP_K_MAX 1024
@@ -113,6 +114,25 @@ int fsamp_workspace_init(void* ws, size_t bytes, hipStream_t stream);
 int fsamp_sample(const void* logits, int dtype, int64_t B, int64_t V, int64_t top_k,
                  double top_p, const float* u, uint64_t seed, uint64_t offset, int64_t* out,
                  void* ws, size_t ws_bytes, int64_t splits_override, hipStream_t stream);
+
+/*
+ * fsamp_sample without a workspace argument, for callers that cannot allocate device memory
+ * (code under HIP graph capture, serving loops, harnesses that forbid allocation).  No
+ * counterpart in the reference.  Split rows use a fixed scratch that the library holds on each
+ * GPU until the process ends (FSAMP_NOALLOC_ROWS * 128 bytes of row tickets plus
+ * FSAMP_NOALLOC_CANDIDATE_BYTES of candidates, 4.125 MiB); a call whose plan needs more (a
+ * split plan with B > FSAMP_NOALLOC_ROWS, or B*splits*k*8 candidate bytes above the limit)
+ * returns FSAMP_ERR_SCRATCH.  Nothing is allocated or freed.  The call takes the device's scratch
+ * address once, at its first call on that device (the current device, which `stream` must
+ * belong to), and clears the tickets there with a fill kernel on `stream`.  Every call on one
+ * GPU shares its scratch: calls that may overlap on one GPU (different streams, concurrent graph
+ * replays) race and must be serialised by the caller.
+ */
+#define FSAMP_NOALLOC_ROWS 1024
+#define FSAMP_NOALLOC_CANDIDATE_BYTES (4u << 20)
+int fsamp_sample_noalloc(const void* logits, int dtype, int64_t B, int64_t V, int64_t top_k,
+                         double top_p, const float* u, uint64_t seed, uint64_t offset,
+                         int64_t* out, int64_t splits_override, hipStream_t stream);
 
 /*
  * Per-row sampling controls and the graph-safe draw of fsamp_sample_ex.  Every pointer may be

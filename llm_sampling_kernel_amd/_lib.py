@@ -75,6 +75,8 @@ SIGNATURES = {
     "fsamp_counter_bytes": (_sz, [_i64]),
     "fsamp_scratch_bytes": (_sz, [_vp, _i64, _i64, _i64, _i64]),
     "fsamp_run": (_i32, [ctypes.c_void_p, _vp]),
+    "fsamp_sample_noalloc": (_i32, [_vp, _i32, _i64, _i64, _i64, _dbl, _vp, _u64, _u64, _vp,
+                                    _i64, _vp]),
     "fsamp_topk_shard": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _sz, _vp, _sz,
                                 _i64, _vp]),
     "fsamp_merge_sample": (_i32, [_vp, _i32, _i64, _i64, _i64, _dbl, _vp, _u64, _u64, _vp, _vp,

@@ -10,6 +10,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include "fsamp.h"
 #include "fsamp_internal.h"
@@ -114,6 +115,40 @@ __global__ void fill_zero_kernel(uint32_t* p, size_t n) {
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
        i += (size_t)gridDim.x * blockDim.x)
     p[i] = 0u;
+}
+
+// ---- fixed scratch of fsamp_sample_noalloc ---------------------------------------------------
+//
+// Device memory the library owns for callers that cannot allocate: FSAMP_NOALLOC_ROWS per-row
+// tickets (128 bytes each) followed by FSAMP_NOALLOC_CANDIDATE_BYTES of split candidates, in a
+// file-scope array that every GPU the library runs on holds once, until the process ends.  In
+// host code `scratch` only names the array (it is no device address): its address on a device
+// comes from hipGetSymbolAddress, taken once per device with that device current, and only that
+// pointer is ever passed to a kernel.  The tickets must be zero before a call and every call
+// leaves them zero; they are cleared once, by a fill kernel, at the first call on a device.
+constexpr size_t kFixedTicketBytes = (size_t)FSAMP_NOALLOC_ROWS * TICKET_STRIDE * 4u;
+constexpr size_t kFixedScratchBytes = kFixedTicketBytes + FSAMP_NOALLOC_CANDIDATE_BYTES;
+static __device__ __align__(256) unsigned char scratch[kFixedScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_fixed_mu;
+void* g_fixed_ptr[kMaxDevices] = {};
+
+// The device's copy of `scratch` (set-up on first use), or nullptr on a HIP error.
+void* fixed_scratch(hipStream_t stream) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_fixed_mu);
+  if (g_fixed_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr)
+      return nullptr;
+    hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)(kFixedTicketBytes / 4 / 256)), dim3(256),
+                       0, stream, static_cast<uint32_t*>(ptr), kFixedTicketBytes / 4);
+    if (hipGetLastError() != hipSuccess) return nullptr;
+    g_fixed_ptr[dev] = ptr;
+  }
+  return g_fixed_ptr[dev];
 }
 
 // One sampler launch, whatever entry point it came through.  The workspace arrives in one of
@@ -273,6 +308,9 @@ const char* fsamp_error_string(int status) {
     case FSAMP_ERR_VOCAB: return "vocabulary too large for the workgroup tiling";
     case FSAMP_ERR_LAUNCH: return "HIP kernel launch failed";
     case FSAMP_ERR_VERSION: return "fsamp_call.struct_bytes does not match this library";
+    case FSAMP_ERR_SCRATCH:
+      return "the call needs more than fsamp_sample_noalloc's fixed scratch (batch above "
+             "FSAMP_NOALLOC_ROWS or split candidates above FSAMP_NOALLOC_CANDIDATE_BYTES)";
     default: return "unknown fsamp status";
   }
 }
@@ -422,6 +460,32 @@ int fsamp_debug_sample_traced(const void* logits, int dtype, int64_t B, int64_t 
   Call c = classic(logits, dtype, B, V, top_k, top_p, u, 0, 0, ws, ws_bytes, splits_override);
   c.out = out;
   c.trace = trace;
+  return launch(c, stream);
+}
+
+int fsamp_sample_noalloc(const void* logits, int dtype, int64_t B, int64_t V, int64_t top_k,
+                         double top_p, const float* u, uint64_t seed, uint64_t offset,
+                         int64_t* out, int64_t splits_override, hipStream_t stream) {
+  if (out == nullptr) return FSAMP_ERR_NULL;
+  int rc = validate(dtype, B, V, top_k);
+  if (rc != FSAMP_OK) return rc;
+  fsamp_plan pl;
+  rc = make_plan_impl(logits, B, V, V, top_k, splits_override, 0, &pl, nullptr);
+  if (rc != FSAMP_OK) return rc;
+  Call c = classic(logits, dtype, B, V, top_k, top_p, u, seed, offset, nullptr, 0,
+                   splits_override);
+  c.out = out;
+  c.split_ws = true;
+  if (pl.splits > 1) {
+    if (B > FSAMP_NOALLOC_ROWS || scratch_bytes_of(pl) > FSAMP_NOALLOC_CANDIDATE_BYTES)
+      return FSAMP_ERR_SCRATCH;
+    char* ptr = static_cast<char*>(fixed_scratch(stream));
+    if (ptr == nullptr) return FSAMP_ERR_LAUNCH;
+    c.counters = ptr;
+    c.counters_bytes = kFixedTicketBytes;
+    c.scratch = ptr + kFixedTicketBytes;
+    c.scratch_bytes = FSAMP_NOALLOC_CANDIDATE_BYTES;
+  }
   return launch(c, stream);
 }
 
