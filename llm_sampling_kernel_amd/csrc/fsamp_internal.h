@@ -69,6 +69,43 @@ struct KernelEntry {
   X(256, 1) X(256, 2) X(256, 3) X(256, 4) X(256, 6) X(256, 8) X(1024, 4) X(1024, 5) \
   X(1024, 6) X(1024, 8)
 
+// Pipelined load of the large register tilings (vector loads, 512 or fewer threads, at least
+// 12,288 vector chunks per workgroup): a thread keeps this many loads in flight, converting chunk
+// c before it issues the next load, so that the selection can start before the slice has landed
+// (the streaming selection in fsamp_kernel.hip).  0 issues every load at once.  On MI355X a
+// 512 x 38 register load of the B=256 batch measured 15.7 us with every load in flight and
+// 14.1-14.3 us at depths 4-12; depths above 6 push the 512 x 38 streaming kernel past 256 VGPRs.
+// The 1024-thread tilings stay unpipelined: their streaming form needs more than the 128 VGPRs a
+// 1024-thread workgroup may use and measured 30.6 us at B=256 against 19.0 us.
+template <int NT, int CH, bool VEC>
+constexpr int pipe_depth() {
+#ifdef FSAMP_PIPE_DEPTH
+  return VEC && NT < 1024 && CH * NT >= 12288 && CH >= 16 ? FSAMP_PIPE_DEPTH : 0;
+#else
+  return !VEC || NT >= 1024 || CH < 16 || CH * NT < 12288 ? 0 : 6;
+#endif
+}
+
+// Chunks whose maxima give the streaming selection its lower bound (even: whole pairs), and the
+// loads issued at once before the bound so that the pipe does not drain while it is computed.
+template <int CH>
+constexpr int stream_bound_chunks() {
+#ifdef FSAMP_STREAM_BOUND
+  return FSAMP_STREAM_BOUND;
+#else
+  return (CH * 2 / 3) & ~1;
+#endif
+}
+
+template <int CH>
+constexpr int stream_extra_loads() {
+#ifdef FSAMP_STREAM_EXTRA
+  return FSAMP_STREAM_EXTRA;
+#else
+  return 4;
+#endif
+}
+
 extern const KernelEntry kKernels[];
 extern const int kNumKernels;
 // fsamp_merge_kernel<RB> for RB = 1, 2, 4, 8, 16

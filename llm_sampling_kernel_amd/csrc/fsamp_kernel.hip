@@ -787,6 +787,13 @@ __device__ __forceinline__ void wave_tail_regs(const Params& p, Smem<NT>& sm, ui
                                                int keff, int row, int split, const RowCtl& rc,
                                                int S);
 
+// 64-bit value of lane `src` (per-lane source), as two 32-bit lane shuffles
+__device__ __forceinline__ uint64_t shfl_u64(uint64_t v, int src) {
+  const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)v, src, 64);
+  const uint32_t hi = (uint32_t)__shfl((int)(uint32_t)(v >> 32), src, 64);
+  return ((uint64_t)hi << 32) | lo;
+}
+
 // Sorts up to 64 candidate words >= L descending, one per lane.  When every candidate key
 // lies in [L, L + 2^14) (L >= 0xC000: the slice's bound sits in the top quarter of the key
 // range, as for any row whose top values are positive) and ids fit in 18 bits, each word is
@@ -802,6 +809,20 @@ __device__ __forceinline__ uint64_t wave_sort64_words(uint64_t v, uint32_t L, in
   uint64_t a[1] = {v};
   wave_sort_desc_n<1>(a);
   return a[0];
+}
+
+// The descending top 64 of up to 128 candidate words >= L (a: candidate l, b: candidate 64 + l,
+// zeros past the end), one per lane.  With every key in [L, L + 2^14) and ids below 2^18 the
+// words are compared as 32-bit (key - L) << 18 | (2^18 - 1 - id), as in wave_sort64_words.
+__device__ __forceinline__ uint64_t wave_top64_of128(uint64_t a, uint64_t b, uint32_t L, int V) {
+  if (L >= 0xC000u && V < (1 << 18)) {
+    auto to32 = [&](uint64_t v) -> uint32_t {
+      return v != 0ull ? ((((uint32_t)(v >> 32) - L) << 18) | (0x3FFFFu - unpack_id(v))) : 0u;
+    };
+    const uint32_t w = wave_top64_of_two<uint32_t>(to32(a), to32(b));
+    return w != 0u ? pack((w >> 18) + L, 0x3FFFFu - (w & 0x3FFFFu)) : 0ull;
+  }
+  return wave_top64_of_two<uint64_t>(a, b);
 }
 
 template <int RB, int NT>
@@ -1089,6 +1110,10 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
   };
   if (t == 0) sm.misc[M_CNT] = 0;
   if (t < 64) sm.top[t] = 0ull;  // the first 64 candidate slots, read whole after the gather
+#ifdef FSAMP_YOUNG_PRIO
+  // experiment: the second wave of each SIMD (waves W/2..W-1) gets issue priority
+  if (wid >= W / 2) __builtin_amdgcn_s_setprio(FSAMP_YOUNG_PRIO);
+#endif
 
   // 1. load the slice into registers as packed keys (padding = key 0).  With VEC, V and the
   //    split bounds are multiples of 8, so a chunk is all in or all out; chunks past the slice
@@ -1121,7 +1146,27 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
       for (int c = 0; c < CH; ++c) kv[c][0] = kv[c][1] = kv[c][2] = kv[c][3] = 0u;
     }
   };
-  load_slice();
+  // one vector chunk (VEC only), c a compile-time index after unrolling
+  auto load_chunk = [&](int c) {
+    const int e0 = lo + (c * NT + t) * 8;
+    const uint4 v = load_stream16(xr + min(e0, hi - 8));
+    kv[c][0] = v.x;
+    kv[c][1] = v.y;
+    kv[c][2] = v.z;
+    kv[c][3] = v.w;
+  };
+  // Streaming selection of the large tilings (SP): loads kept PD deep, the lower bound taken
+  // from the first PB chunks, then PX more loads issued at once to cover the bound, and every
+  // later chunk's candidates gathered as it lands (see the streaming block below).
+  constexpr int PD = pipe_depth<NT, CH, VEC>();  // loads in flight (0: every load issued at once)
+  constexpr bool SP = PD > 0;
+  constexpr int PX = SP ? stream_extra_loads<CH>() : 0;
+  constexpr int PB = SP ? (stream_bound_chunks<CH>() < ((CH - PD - PX) & ~1)
+                               ? stream_bound_chunks<CH>()
+                               : ((CH - PD - PX) & ~1))
+                        : CH;
+  static_assert(!SP || (PB >= 2 && PB % 2 == 0 && PB + PD + PX <= CH), "streaming plan");
+  if constexpr (!SP) load_slice();
   // pm[i]: packed 16-bit maxima over the two chunks of pair i (even halves, odd halves); a
   // pair holds an element >= X iff pkmax(pm[i], (X-1) in both halves) differs from the latter
   uint32_t pm[NP];
@@ -1225,8 +1270,11 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
       }
     }
   };
-  auto extract = [&](uint32_t L, int nst, uint64_t* region_base, int rw, int32_t* wc) {
-    constexpr int C0 = 0, C1 = CH;
+  // wc != nullptr: each wave takes its slots of region_base with one LDS atomic on *wc;
+  // wc == nullptr: region_base is the wave's own region and wcnt its wave-uniform count
+  auto extract = [&](auto c0c, auto c1c, uint32_t L, int nst, uint64_t* region_base, int rw,
+                     int32_t* wc, int& wcnt) {
+    constexpr int C0 = decltype(c0c)::value, C1 = decltype(c1c)::value;
     FSAMP_TRACE(13);
     const bool from_regs = nst > STAGE_SLOTS;
     auto staged_mask = [&](int s) -> uint32_t {
@@ -1252,9 +1300,15 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
     FSAMP_TRACE(10);
     if (__ballot(mine > 0) != 0ull) {
       const uint32_t incl = wave_incl_scan_u32((uint32_t)mine);
-      int base = 0;
-      if (lane == 63) base = atomicAdd(wc, (int)incl);
-      int slot = __builtin_amdgcn_readlane(base, 63) + (int)incl - mine;
+      int slot;
+      if (wc != nullptr) {
+        int base = 0;
+        if (lane == 63) base = atomicAdd(wc, (int)incl);
+        slot = __builtin_amdgcn_readlane(base, 63) + (int)incl - mine;
+      } else {
+        slot = wcnt + (int)incl - mine;
+        wcnt += __builtin_amdgcn_readlane((int)incl, 63);
+      }
       uint64_t* region = region_base;
       FSAMP_TRACE(11);
       if (from_regs) {
@@ -1295,10 +1349,173 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
     FSAMP_TRACE(12);
   };
 
+  // candidates >= L of chunk pair i into this wave's region (capacity REG): slots from a ballot
+  // and its mbcnt over the wave-uniform count; used for the last pair of the streaming path,
+  // whose data lands last (one compare and one scalar branch when the wave has no candidate)
+  constexpr int REG = FSAMP_K_MAX / W;
+  auto gather_pair = [&](auto ic, uint32_t L, int& wcnt, uint64_t* region) {
+    constexpr int i = decltype(ic)::value;
+    constexpr int c0 = 2 * i, c1 = 2 * i + 1;
+    const uint32_t lm1 = (L - 1u) * 0x10001u;
+    const bool hit = pkmax(pm[i], lm1) != lm1;
+    if (__ballot(hit) == 0ull) return;
+    uint32_t m = 0u;
+    if (hit) {
+      m = ge_mask(kv[c0], L);
+      if constexpr (c1 < CH) m |= ge_mask(kv[c1], L) << 8;
+    }
+    const uint32_t idb = opaque_base(lo, t);
+    for (;;) {
+      const uint64_t act = __ballot(m != 0u);
+      if (act == 0ull) break;
+      if (m != 0u) {
+        const int j = __ffs(m) - 1;
+        m &= m - 1u;
+        uint32_t key;
+        if constexpr (c1 < CH)
+          key = key_of16(kv[c0][0], kv[c0][1], kv[c0][2], kv[c0][3], kv[c1][0], kv[c1][1],
+                         kv[c1][2], kv[c1][3], j);
+        else
+          key = key_at(kv[c0], j);
+        const uint32_t id = idb + (uint32_t)((c0 + (j >> 3)) * NT * 8 + (j & 7));
+        const int below = (int)__builtin_amdgcn_mbcnt_hi(
+            (uint32_t)(act >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)act, 0u));
+        const int slot = wcnt + below;
+        if (slot < REG) region[slot] = pack(key, id);
+      }
+      wcnt += (int)__popcll(act);
+    }
+  };
+
+  // Load order of the streaming tilings: PD loads, then one more after each conversion up to
+  // chunk PB-1; PX more at once before the bound; then load c + PD + PX after converting c.
+  auto stream_loads_head = [&]() {
+    static_for<0, PD>([&](auto cc) { load_chunk(decltype(cc)::value); });
+    static_for<0, PB>([&](auto cc) {
+      constexpr int c = decltype(cc)::value;
+      __builtin_amdgcn_sched_barrier(0);
+      convert(c);
+      __builtin_amdgcn_sched_barrier(0);
+      load_chunk(c + PD);
+    });
+    static_for<PB + PD, PB + PD + PX>([&](auto cc) { load_chunk(decltype(cc)::value); });
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // the rest of the slice without a gather (ablation stops, wide k, fallback)
+  auto stream_loads_tail = [&]() {
+    static_for<PB, CH>([&](auto cc) {
+      constexpr int c = decltype(cc)::value;
+      __builtin_amdgcn_sched_barrier(0);
+      convert(c);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (c + PD + PX < CH) load_chunk(c + PD + PX);
+    });
+    FSAMP_WTRACE(pm[NP - 1]);
+  };
+
+  if constexpr (SP) {
+    if (count > 0) {
+      stream_loads_head();
+    } else {
 #pragma unroll
-  for (int c = 0; c < CH; ++c) convert(c);
+      for (int c = 0; c < CH; ++c) kv[c][0] = kv[c][1] = kv[c][2] = kv[c][3] = 0u;
+#pragma unroll
+      for (int c = 0; c < PB; ++c) convert(c);
+    }
+    // Streaming selection for k <= 64 (every condition is uniform over the workgroup):
+    //   L = the lower bound from the maxima of chunks 0..PB-1 (valid for the whole slice: the
+    //   prefix alone holds keff distinct elements >= L); the prefix's candidates are staged and
+    //   gathered while the last loads are in flight, the rest once it has landed; wave 0 then
+    //   takes the top 64 of the (on C5, 70 to 124) candidates in registers.  More than 128
+    //   falls back to the general selection below with the bound of the whole slice.
+    if (count > 0 && keff <= 64 && p.stop >= 2) {
+      const uint32_t L = lower_bound(tmax_of(IC<0>{}, IC<PB / 2>{}));
+      if (p.stop == 2) {
+        stream_loads_tail();
+        if (t == 0 && split == 0) p.out[row] = (int64_t)L;
+        return;
+      }
+      // Candidates go to per-wave regions of top[] (REG words each) at a wave-uniform count:
+      // the prefix's, staged through LDS while the last loads are in flight; the middle pairs'
+      // (staged one by one as each lands, gathered while the last pair is still in flight);
+      // then the last pair's straight from registers, the only gather after the last byte.
+      int wcnt = 0;
+      uint64_t* region = sm.top + wid * REG;
+      int nst = 0;
+      stage(IC<0>{}, IC<PB / 2>{}, L, nst);
+      extract(IC<0>{}, IC<PB>{}, L, nst, region, REG, nullptr, wcnt);
+      constexpr int LASTP = NP - 1;  // the last pair (chunk 2*LASTP, and 2*LASTP + 1 if < CH)
+      int nst2 = 0;
+      static_for<PB, CH>([&](auto cc) {
+        constexpr int c = decltype(cc)::value;
+        __builtin_amdgcn_sched_barrier(0);
+        convert(c);
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (c + PD + PX < CH) load_chunk(c + PD + PX);
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (((c & 1) == 1 || c == CH - 1) && c / 2 < LASTP)
+          stage(IC<c / 2>{}, IC<c / 2 + 1>{}, L, nst2);
+        if constexpr (c == 2 * LASTP - 1)  // every middle pair staged: gather them
+          extract(IC<PB>{}, IC<2 * LASTP>{}, L, nst2, region, REG, nullptr, wcnt);
+      });
+      FSAMP_WTRACE(pm[NP - 1]);
+      gather_pair(IC<LASTP>{}, L, wcnt, region);
+      if (lane == 0) sm.wsum[0][wid] = wcnt;
+      __syncthreads();
+      FSAMP_TRACE(4);
+      int cend[W];  // inclusive prefix of the per-wave counts
+      int total = 0;
+      bool full = false;
+#pragma unroll
+      for (int w = 0; w < W; ++w) {
+        const int cw = __builtin_amdgcn_readfirstlane(sm.wsum[0][w]);
+        full = full || cw > REG;
+        total += cw;
+        cend[w] = total;
+      }
+      if (p.stop == 3) {
+        if (t == 0 && split == 0) p.out[row] = total;
+        return;
+      }
+      if (!full && total <= 128) {
+        if (wid != 0) return;
+        // candidate e of the concatenated regions
+        auto cand = [&](int e) -> uint64_t {
+          if (e >= total) return 0ull;
+          int w = 0, base = 0;
+#pragma unroll
+          for (int r = 0; r + 1 < W; ++r) {
+            if (e >= cend[r]) {
+              w = r + 1;
+              base = cend[r];
+            }
+          }
+          return sm.top[w * REG + (e - base)];
+        };
+        FSAMP_TRACE(14);
+        uint64_t v[1];
+        if (total <= 64) v[0] = wave_sort64_words(cand(lane), L, p.V);
+        else v[0] = wave_top64_of128(cand(lane), cand(64 + lane), L, p.V);
+        if (lane >= keff) v[0] = 0ull;
+        const RowCtl rc = row_ctl();
+        wave_tail_regs<1, NT>(p, sm, v, keff, row, split, rc, p.S);
+        return;
+      }
+      // too many candidates for the register sort: the general selection, full bound.  Every
+      // wave has read the total before the counter is cleared for the general gather.
+      __syncthreads();
+      if (t == 0) sm.misc[M_CNT] = 0;
+    } else {
+      if (count > 0) stream_loads_tail();
+      else
+        static_for<PB, CH>([&](auto cc) { convert(decltype(cc)::value); });
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < CH; ++c) convert(c);
+  }
   const uint32_t tmax = tmax_of(IC<0>{}, IC<NP>{});
-  FSAMP_WTRACE(tmax);
+  if constexpr (!SP) FSAMP_WTRACE(tmax);
 
   if (p.stop == 1) {
     const uint32_t wmax = wave_max_u32(tmax);
@@ -1325,7 +1542,8 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
     }
     int nst = 0;
     stage(IC<0>{}, IC<NP>{}, L, nst);
-    extract(L, nst, sm.top, FSAMP_K_MAX, &sm.misc[M_CNT]);
+    int unused = 0;
+    extract(IC<0>{}, IC<CH>{}, L, nst, sm.top, FSAMP_K_MAX, &sm.misc[M_CNT], unused);
     __syncthreads();
     pre = sm.top[lane];  // issued with the count read below: one LDS round trip for both
     L_sel = L;

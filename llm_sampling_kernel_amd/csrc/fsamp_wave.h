@@ -75,10 +75,10 @@ __device__ __forceinline__ uint64_t xor_lane64(uint64_t v) {
 //   For 32-bit values max and min are single VALU ops and the lane-constant select follows
 // (no scalar step in the dependency chain); for 64-bit values one compare, xor-ed with the
 // lane-constant predicate, picks the partner or not.
-template <int K, int J, typename T>
+template <int K, int J, typename T, bool ASC = false>
 __device__ __forceinline__ T bitonic_step(T v) {
   const int l = lane_id();
-  const bool keep_hi = ((l & J) == 0) == ((l & K) == 0);
+  const bool keep_hi = (((l & J) == 0) == ((l & K) == 0)) != ASC;
   if constexpr (sizeof(T) == 8) {
     const T o = (T)xor_lane64<J>((uint64_t)v);
     return ((o > v) == keep_hi) ? o : v;
@@ -89,23 +89,40 @@ __device__ __forceinline__ T bitonic_step(T v) {
   }
 }
 
-template <int K, int J, typename T>
+template <int K, int J, typename T, bool ASC = false>
 __device__ __forceinline__ T bitonic_merge_stages(T v) {
-  v = bitonic_step<K, J>(v);
-  if constexpr (J > 1) v = bitonic_merge_stages<K, J / 2>(v);
+  v = bitonic_step<K, J, T, ASC>(v);
+  if constexpr (J > 1) v = bitonic_merge_stages<K, J / 2, T, ASC>(v);
   return v;
 }
 
-template <int K, typename T>
+template <int K, typename T, bool ASC = false>
 __device__ __forceinline__ T bitonic_levels(T v) {
-  if constexpr (K > 2) v = bitonic_levels<K / 2>(v);
-  return bitonic_merge_stages<K, K / 2>(v);
+  if constexpr (K > 2) v = bitonic_levels<K / 2, T, ASC>(v);
+  return bitonic_merge_stages<K, K / 2, T, ASC>(v);
 }
 
 // Full descending sort of one value per lane (64 values): lane 0 gets the largest.
 template <typename T>
 __device__ __forceinline__ T wave_sort_desc(T v) {
-  return bitonic_levels<64>(v);
+  return bitonic_levels<64, T>(v);
+}
+
+// Full ascending sort of one value per lane (every comparator mirrored): lane 0 the smallest.
+template <typename T>
+__device__ __forceinline__ T wave_sort_asc(T v) {
+  return bitonic_levels<64, T, true>(v);
+}
+
+// The descending top 64 of two lists of 64 values, one of each per lane: a sorted descending,
+// b ascending, the elementwise maximum is a bitonic sequence holding exactly the 64 largest of
+// both, and the six half-cleaner stages of the last bitonic level sort it.
+template <typename T>
+__device__ __forceinline__ T wave_top64_of_two(T a, T b) {
+  a = wave_sort_desc<T>(a);
+  b = wave_sort_asc<T>(b);
+  const T m = a > b ? a : b;
+  return bitonic_merge_stages<64, 32, T>(m);
 }
 
 // Inclusive prefix sum over the 64 lanes in a fixed association: Kogge-Stone inside each

@@ -795,3 +795,36 @@ def test_shard_and_merge_argument_checks():
         fused_sampling.merge_sample(w, _lib.DTYPE_BF16, 0.0)
     with pytest.raises(RuntimeError, match="contiguous int64"):
         fused_sampling.merge_sample(w.float(), _lib.DTYPE_BF16, 0.5)
+
+
+# --- large batches: the streaming selection of the big register tilings --------------------------
+
+def _streaming_rows(V, seed):
+    """128 rows that drive the streaming selection through each of its branches: plain noise,
+    a 64-value tie grid (candidates overflow the register sort: the general path), ascending
+    values (every candidate lands in the last chunks, after the bound), equal values, and a few
+    spikes placed in the first and in the last chunks of a row."""
+    g = np.random.Generator(np.random.PCG64(seed))
+    x = g.standard_normal((128, V)).astype(np.float32) * 3.0
+    grid = np.linspace(-8, 8, 64, dtype=np.float32)
+    x[16:32] = grid[g.integers(0, 64, (16, V))]
+    x[32:40] = np.linspace(-4, 4, V, dtype=np.float32)[None, :]
+    x[40:44] = 0.5
+    x[44:52, :64] += 20.0
+    x[52:60, -64:] += 20.0
+    return x
+
+
+@pytest.mark.parametrize("V", [151936, 128256])
+@pytest.mark.parametrize("k", [1, 20, 50, 64, 65])
+def test_large_batch_rows_through_the_streaming_selection(V, k):
+    bits = W.to_bits(_streaming_rows(V, 8100 + k), "bfloat16")
+    x = dev(bits, "bfloat16")
+    assert fused_sampling.make_plan(x, k).splits == 1
+    un = ustream(128, 8200 + k)
+    want = oracle(bits, "bfloat16", k, 0.9, un)
+    assert np.array_equal(fused.topk_fused(x, k).cpu().numpy(), want.topk_ids)
+    tok, ids, keep, ren = run_u(x, k, 0.9, un)
+    assert np.array_equal(tok, want.token_ids)
+    assert np.array_equal(keep, want.keep)
+    assert np.array_equal(ren.view(np.uint32), want.renormed.view(np.uint32))
