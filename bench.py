@@ -298,6 +298,38 @@ def c5_cold_only(steps: int, warmup: int) -> int:
     return 0
 
 
+def vocab_parallel(x, c, fix_tokens, n_shards: int = 8) -> dict:
+    """The vocabulary-parallel form of one configuration on one GPU: the row cut into n_shards
+    column shards (each what one GPU of a tensor-parallel LM head would hold), the shard
+    selection (fused_sampling.topk_shard) timed on one shard, the merge of the n_shards sorted
+    lists and the draw (fused_sampling.merge_sample) timed on their stack; the merged tokens are
+    checked against the whole-row fixture."""
+    import torch
+
+    from llm_sampling_kernel_amd import _lib, fused_sampling
+
+    B, V = x.shape
+    vs = V // n_shards
+    bounds = [(i * vs, (i + 1) * vs if i + 1 < n_shards else V) for i in range(n_shards)]
+    words = torch.stack([fused_sampling.topk_shard(x[:, lo:hi], c.top_k, lo) for lo, hi in bounds],
+                        dim=1).contiguous()
+    code = _lib.DTYPE_BF16 if c.dtype == "bfloat16" else _lib.DTYPE_F16
+    u = torch.from_numpy(c.u).cuda()
+    tok = fused_sampling.merge_sample(words, code, c.top_p, u).cpu().numpy()
+    if not np.array_equal(tok, fix_tokens):
+        raise RuntimeError(f"{c.name}: merged shard tokens differ from the fixture")
+    lo, hi = bounds[0]
+    shard = x[:, lo:hi]
+    t_shard = calibrated_ms(lambda: fused_sampling.topk_shard(shard, c.top_k, lo), warmup=20,
+                            window=50.0, reps=5)["ms"] * 1e3
+    t_merge = calibrated_ms(lambda: fused_sampling.merge_sample(words, code, c.top_p, u),
+                            warmup=20, window=50.0, reps=5)["ms"] * 1e3
+    return {"shards": n_shards, "shard_columns": vs, "merge_width": n_shards * c.top_k,
+            "us_per_shard_call": round(t_shard, 3), "us_per_merge_call": round(t_merge, 3),
+            "note": "one shard's selection (sorted candidate words with global ids) and the merge "
+                    "of the shards' lists plus the draw; no collective on one GPU"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -436,6 +468,12 @@ def main() -> int:
     log(f"C1 {c1_us:.2f} us/call eager, {c1_graph_us:.2f} graph; floor {floor_us:.2f} / "
         f"{floor_graph_us:.2f}; launches per call {lc1.get('launches_per_call')}")
 
+    vp = {}
+    for name, xc_ in (("C1", x1), ("C5", x0)):
+        vp[name] = vocab_parallel(xc_, W.case(name), fix[f"{name}/token_ids"])
+        log(f"{name} vocabulary-parallel: shard {vp[name]['us_per_shard_call']:.2f} us, merge "
+            f"{vp[name]['us_per_merge_call']:.2f} us")
+
     # the other benchmark configurations, eager back-to-back calls (hot: one buffer each)
     others = {}
     for name in ("C2_B1_k20", "C2_B1_k50", "C2_B4_k50", "C2_B16_k50", "C2_B64_k20",
@@ -511,11 +549,13 @@ def main() -> int:
                                   "row-block scan)"},
         "c5_load_floor": {"us_per_call": round(ms_load * 1e3, 3),
                           "gbps": round(gb5 / (ms_load * 1e-3) / 1e9, 1),
-                          "note": "fsamp_probe_load: the sampler's B=256 launch shape (512 "
-                                  "threads, 38 nontemporal 16-byte loads each) with only a "
-                                  "per-wave maximum after the loads"},
+                          "note": "fsamp_probe_load: the sampler's B=256 launch shape and load "
+                                  "order (512 threads, 38 nontemporal 16-byte loads each, 6 in "
+                                  "flight, the slice kept in registers) with only a per-wave "
+                                  "maximum after the loads"},
         "c5_launches": lc5,
         "configs": others,
+        "vocab_parallel": vp,
         "c1": {"us_per_call": round(c1_us, 3), "us_per_call_graph": round(c1_graph_us, 3),
                "launches": lc1, "launch_floor_us": round(floor_us, 3),
                "launch_floor_graph_us": round(floor_graph_us, 3),

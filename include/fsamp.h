@@ -285,7 +285,8 @@ int fsamp_probe_scan_rowblock(const void* logits, int dtype, int64_t B, int64_t 
 
 /* Load-only floor of the sampler's large-batch launch shape (no counterpart in the reference):
  * one 512-thread workgroup per row reads the row with 38 nontemporal 16-byte loads per thread,
- * all in flight at once, and each of its 8 waves writes the largest order key of its share to
+ * issued as the sampler issues them (6 in flight), and each of its 8 waves writes the largest
+ * order key of its share to
  * wave_max[b*8 + w] (device, B*8 uint32).  Needs a 16-byte-aligned base, V % 8 == 0 and
  * V <= 155648 (FSAMP_ERR_VOCAB otherwise). */
 int fsamp_probe_load(const void* logits, int dtype, int64_t B, int64_t V, uint32_t* wave_max,

@@ -74,7 +74,8 @@ struct KernelEntry {
 // c before it issues the next load, so that the selection can start before the slice has landed
 // (the streaming selection in fsamp_kernel.hip).  0 issues every load at once.  On MI355X a
 // 512 x 38 register load of the B=256 batch measured 15.7 us with every load in flight and
-// 14.1-14.3 us at depths 4-12; depths above 6 push the 512 x 38 streaming kernel past 256 VGPRs.
+// 14.1-14.3 us at depths 4-12; the streaming sampler measured 18.78 / 18.99 us at depths 4 / 6,
+// and depths above 6 push the 512 x 38 streaming kernel past 256 VGPRs.
 // The 1024-thread tilings stay unpipelined: their streaming form needs more than the 128 VGPRs a
 // 1024-thread workgroup may use and measured 30.6 us at B=256 against 19.0 us.
 template <int NT, int CH, bool VEC>
@@ -82,7 +83,7 @@ constexpr int pipe_depth() {
 #ifdef FSAMP_PIPE_DEPTH
   return VEC && NT < 1024 && CH * NT >= 12288 && CH >= 16 ? FSAMP_PIPE_DEPTH : 0;
 #else
-  return !VEC || NT >= 1024 || CH < 16 || CH * NT < 12288 ? 0 : 6;
+  return !VEC || NT >= 1024 || CH < 16 || CH * NT < 12288 ? 0 : 4;
 #endif
 }
 

@@ -890,12 +890,12 @@ __device__ __forceinline__ void wave_tail_regs(const Params& p, Smem<NT>& sm, ui
 
   if (S > 1) {
     // 5. hand the slice's sorted top-K to the row's last workgroup.  The words are written
-    //    with agent-scope atomic stores, which write through to the device-coherent level,
-    //    and s_waitcnt(0) holds the wave until every one of them is acknowledged before the
-    //    arrival counter is bumped; the last workgroup reads them back with agent-scope atomic
-    //    loads, which bypass the (per-XCD, non-coherent) L2.  That is the release / acquire
-    //    pair without an L2 writeback or invalidate: on gfx950 a __threadfence costs ~1.5 us
-    //    more per hand-off and the writebacks serialise across workgroups.
+    //    with agent-scope atomic stores, s_waitcnt(0) holds the wave until every one of them is
+    //    acknowledged, and the row's ticket is taken with an acquire-release agent-scope
+    //    fetch_add, which orders the stores before the increment and the last arriver's reads
+    //    of the other lists (agent-scope atomic loads) after it.  On MI355X the acquire-release
+    //    ticket measured the same as a relaxed one here (10.05 against 10.07 us at B=1, six
+    //    splits); a full __threadfence costs ~1.5 us more per hand-off.
     uint64_t* dst = p.partials + ((size_t)row * S + split) * p.K;
 #pragma unroll
     for (int i = 0; i < RB; ++i) {
@@ -905,7 +905,7 @@ __device__ __forceinline__ void wave_tail_regs(const Params& p, Smem<NT>& sm, ui
     __builtin_amdgcn_s_waitcnt(0);
     unsigned prev = 0;
     if (l == 0)
-      prev = __hip_atomic_fetch_add(&p.tickets[row * TICKET_STRIDE], 1u, __ATOMIC_RELAXED,
+      prev = __hip_atomic_fetch_add(&p.tickets[row * TICKET_STRIDE], 1u, __ATOMIC_ACQ_REL,
                                     __HIP_MEMORY_SCOPE_AGENT);
     prev = read_lane_u32(prev, 0);
     FSAMP_TRACE(6);
@@ -964,7 +964,7 @@ __device__ __forceinline__ void wave_back_wide(const Params& p, Smem<NT>& sm, in
     __builtin_amdgcn_s_waitcnt(0);
     unsigned prev = 0;
     if (l == 0)
-      prev = __hip_atomic_fetch_add(&p.tickets[row * TICKET_STRIDE], 1u, __ATOMIC_RELAXED,
+      prev = __hip_atomic_fetch_add(&p.tickets[row * TICKET_STRIDE], 1u, __ATOMIC_ACQ_REL,
                                     __HIP_MEMORY_SCOPE_AGENT);
     prev = read_lane_u32(prev, 0);
     FSAMP_TRACE(6);
@@ -1110,10 +1110,6 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
   };
   if (t == 0) sm.misc[M_CNT] = 0;
   if (t < 64) sm.top[t] = 0ull;  // the first 64 candidate slots, read whole after the gather
-#ifdef FSAMP_YOUNG_PRIO
-  // experiment: the second wave of each SIMD (waves W/2..W-1) gets issue priority
-  if (wid >= W / 2) __builtin_amdgcn_s_setprio(FSAMP_YOUNG_PRIO);
-#endif
 
   // 1. load the slice into registers as packed keys (padding = key 0).  With VEC, V and the
   //    split bounds are multiples of 8, so a chunk is all in or all out; chunks past the slice
@@ -1204,24 +1200,67 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
     return pkmax(pm[c >> 1], xm1) != xm1;
   };
 
+  // Lower bound for keff > 256 (wide k): the keff-th largest of the 8-element group maxima --
+  // the two 16-bit halves of every pair maximum pm[i] (even and odd positions of the pair's two
+  // chunks), 2 * NP per thread -- found exactly by a two-round radix select over LDS histograms
+  // of those maxima only.  The groups are disjoint, so at least keff distinct elements are >= it.
+  // On the C4 k=1024 rows this admits ~1.1k candidates per split, where the minimum of the
+  // thread maxima admits ~7k.  With fewer than keff non-empty groups every element qualifies.
+  auto group_bound = [&]() -> uint32_t {
+    const int sub = wid & (NSUB - 1);
+    zero_hist<NT>(sm.u.rx.hist);
+    __syncthreads();
+    FSAMP_TRACE(2);
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      const uint32_t g0 = pm[i] & 0xFFFFu, g1 = pm[i] >> 16;
+      wave_add(sm.u.rx.hist + sub * 256, g0 >> 8, g0 != 0u);
+      wave_add(sm.u.rx.hist + sub * 256, g1 >> 8, g1 != 0u);
+    }
+    __syncthreads();
+    fold_hist<NT>(sm.u.rx.hist);
+    __syncthreads();
+    suffix256(sm.u.rx.hist, sm.u.rx.suf);
+    __syncthreads();
+    const int groups = __builtin_amdgcn_readfirstlane((int)sm.u.rx.suf[0]);
+    if (groups < keff) return 1u;  // uniform: every thread read the same total
+    find_bucket<NT>(sm.u.rx.suf, keff, 0, &sm.misc[M_HB], &sm.misc[M_ABOVE]);
+    __syncthreads();
+    const uint32_t hb = (uint32_t)__builtin_amdgcn_readfirstlane(sm.misc[M_HB]);
+    const int above = __builtin_amdgcn_readfirstlane(sm.misc[M_ABOVE]);
+    zero_hist<NT>(sm.u.rx.hist);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      const uint32_t g0 = pm[i] & 0xFFFFu, g1 = pm[i] >> 16;
+      wave_add(sm.u.rx.hist + sub * 256, g0 & 255u, g0 != 0u && (g0 >> 8) == hb);
+      wave_add(sm.u.rx.hist + sub * 256, g1 & 255u, g1 != 0u && (g1 >> 8) == hb);
+    }
+    __syncthreads();
+    fold_hist<NT>(sm.u.rx.hist);
+    __syncthreads();
+    suffix256(sm.u.rx.hist, sm.u.rx.suf);
+    __syncthreads();
+    find_bucket<NT>(sm.u.rx.suf, keff - above, above, &sm.misc[M_LB], &sm.misc[M_GT]);
+    __syncthreads();
+    FSAMP_TRACE(3);
+    const uint32_t lb = (uint32_t)__builtin_amdgcn_readfirstlane(sm.misc[M_LB]);
+    return max((hb << 8) | lb, 1u);
+  };
+
   // 2. lower bound L of the keff-th largest key among the given thread maxima (keff <= NT by
   //    plan): the keff-th largest of the union of every wave's top-m thread maxima,
   //    m = max(ceil(keff/W), 64/W).  Maxima are made unique by the thread index in the low
   //    bits.  Each wave sorts its 64 maxima with the DPP network and publishes the top m;
   //    after one barrier every wave sorts the W*m published words itself (no second barrier).
-  //    Past 256 published words (keff > 256, where the candidates go through the radix select
-  //    anyway) the looser bound min over waves of the wave's m-th maximum is used instead:
-  //    every wave then has m threads, W*m >= keff in all, whose maximum is >= L.  It keeps the
-  //    register sort of more than 256 words out of the phase that still holds the slice.
+  //    Past 256 published words (keff > 256) the group bound above is used instead, which
+  //    keeps the register sort of more than 256 words out of the phase that holds the slice.
   auto lower_bound = [&](uint32_t tm) -> uint32_t {
     const int m = min(64, max((keff + W - 1) / W, 64 / W));
     const int n = W * m;
+    if (n > WSORT_MAX) return group_bound();
     const uint32_t srt = wave_sort_desc<uint32_t>((tm << 10) | (uint32_t)t);
-    if (n <= WSORT_MAX) {
-      if (lane < m) sm.u.lb[wid * m + lane] = srt;
-    } else {
-      if (lane == m - 1) sm.u.lb[wid] = srt;
-    }
+    if (lane < m) sm.u.lb[wid * m + lane] = srt;
     __syncthreads();
     FSAMP_TRACE(2);
     uint32_t kth;
@@ -1229,12 +1268,8 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
       kth = wave_kth_u32<1>(sm.u.lb, n, keff);
     } else if (n <= 128) {
       kth = wave_kth_u32<2>(sm.u.lb, n, keff);
-    } else if (n <= WSORT_MAX) {
-      kth = wave_kth_u32<4>(sm.u.lb, n, keff);
     } else {
-      kth = lane < W ? sm.u.lb[lane] : 0xFFFFFFFFu;
-#pragma unroll
-      for (int d = 1; d < 64; d <<= 1) kth = min(kth, (uint32_t)__shfl_xor((int)kth, d, 64));
+      kth = wave_kth_u32<4>(sm.u.lb, n, keff);
     }
     FSAMP_TRACE(3);
     return max(kth >> 10, 1u);
@@ -1685,8 +1720,13 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
   // 5-6'. Rows split over several workgroups with k > 128: the whole workgroup hands the
   //    slice's sorted list over and, in the row's last workgroup, reads the S lists back and
   //    folds them (workgroup bitonic merges), where one wave would take S-1 wide merges and
-  //    S*K serial loads.  The protocol is the one of the wave-0 path below: agent-scope
-  //    atomic stores, each wave waiting for its own, then one ticket for the workgroup.
+  //    S*K serial loads.  The words are agent-scope atomic stores, each wave waits for its
+  //    own (s_waitcnt 0) before the workgroup barrier, and one relaxed agent-scope ticket
+  //    follows.  This relies on a gfx950 property the HIP memory model does not state: an
+  //    agent-scope atomic store is written through to the device-coherent level (sc1) and is
+  //    visible to every agent-scope atomic load once s_waitcnt has seen it acknowledged.  An
+  //    acquire-release ticket here measured 0.7 us slower (C4-like k=256: 22.67 against
+  //    21.93 us), so the relaxed form stays; the wave-0 hand-off, where it is free, uses it.
   //    Compiled only into the MERGE instantiations, which the host launches for exactly those
   //    calls: the code would otherwise cost the common path (k <= 128) ~0.1-0.2 us.
   bool merged = false;

@@ -182,11 +182,13 @@ __global__ __launch_bounds__(64) void merge_partial_kernel(const uint64_t* __res
 }
 
 // Load-only floor of the sampler's B=256 launch shape: one 512-thread workgroup per row, every
-// thread issues its LOAD_CH nontemporal dwordx4 loads at once (chunk c of thread t at vector
-// c*512 + t, as the sampler lays its slice out), converts them to packed order keys and keeps
-// their packed maximum; each wave then writes the maximum key of its share (no barrier, no LDS),
-// so the kernel's time is the row read itself plus the launch.
-constexpr int LOAD_NT = 512, LOAD_CH = 38;
+// thread reads its LOAD_CH nontemporal dwordx4 chunks (chunk c of thread t at vector c*512 + t,
+// as the sampler lays its slice out) the way the sampler issues them -- LOAD_DEPTH loads in
+// flight, chunk c converted to packed order keys before load c + LOAD_DEPTH is issued -- and
+// keeps every converted chunk in registers to the end, as the sampler does; each wave then writes
+// the maximum key of its share (no barrier, no LDS), so the kernel's time is the row read itself
+// plus the launch.
+constexpr int LOAD_NT = 512, LOAD_CH = 38, LOAD_DEPTH = 6;
 
 __global__ __launch_bounds__(LOAD_NT) void load_rows_kernel(const uint16_t* __restrict__ x,
                                                             uint32_t* __restrict__ wave_max,
@@ -195,22 +197,33 @@ __global__ __launch_bounds__(LOAD_NT) void load_rows_kernel(const uint16_t* __re
   const int nvec = V >> 3;
   const int t = threadIdx.x;
   uint32_t k[LOAD_CH][4];
-#pragma unroll
-  for (int c = 0; c < LOAD_CH; ++c) {
-    const int i = c * LOAD_NT + t;
-    const uint4 v = load_stream16(rv + min(i, nvec - 1));
+  auto load = [&](int c) {
+    const uint4 v = load_stream16(rv + min(c * LOAD_NT + t, nvec - 1));
     k[c][0] = v.x;
     k[c][1] = v.y;
     k[c][2] = v.z;
     k[c][3] = v.w;
-  }
+  };
+#pragma unroll
+  for (int c = 0; c < LOAD_DEPTH; ++c) load(c);
   uint32_t m = 0;
 #pragma unroll
   for (int c = 0; c < LOAD_CH; ++c) {
+    __builtin_amdgcn_sched_barrier(0);
     const bool in = c * LOAD_NT + t < nvec;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) m = pkmax(m, in ? keys2(k[c][q]) : 0u);
+    for (int q = 0; q < 4; ++q) {
+      k[c][q] = in ? keys2(k[c][q]) : 0u;
+      m = pkmax(m, k[c][q]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (c + LOAD_DEPTH < LOAD_CH) load(c + LOAD_DEPTH);
   }
+  // every converted key stays live to here, as the sampler keeps its slice
+  uint32_t live = 0;
+#pragma unroll
+  for (int c = 0; c < LOAD_CH; ++c) live ^= k[c][0] ^ k[c][1] ^ k[c][2] ^ k[c][3];
+  asm volatile("" ::"v"(live));
   uint32_t mk = max(m & 0xFFFFu, m >> 16);
 #pragma unroll
   for (int d = 32; d > 0; d >>= 1) mk = max(mk, (uint32_t)__shfl_xor((int)mk, d, 64));

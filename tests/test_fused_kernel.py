@@ -828,3 +828,18 @@ def test_large_batch_rows_through_the_streaming_selection(V, k):
     assert np.array_equal(tok, want.token_ids)
     assert np.array_equal(keep, want.keep)
     assert np.array_equal(ren.view(np.uint32), want.renormed.view(np.uint32))
+
+
+def test_sixteen_split_hand_off_at_b256():
+    # the most workgroups per row (16) on the largest batch: 4096 workgroups whose row
+    # tickets and candidate lists must hand over exactly once per row
+    bits = randn_bits((256, 20000), 8300, 3.0, "bfloat16")
+    x = dev(bits, "bfloat16")
+    assert fused_sampling.make_plan(x, 50, 16).splits == 16
+    un = ustream(256, 8301)
+    want = oracle(bits, "bfloat16", 50, 0.9, un)
+    tok, tok_stages, keep, ren = run_u(x, 50, 0.9, un, 16)
+    assert np.array_equal(tok_stages, tok)
+    assert np.array_equal(fused.topk_fused(x, 50, 16).cpu().numpy(), want.topk_ids)
+    assert np.array_equal(tok, want.token_ids)
+    assert np.array_equal(ren.view(np.uint32), want.renormed.view(np.uint32))
