@@ -142,6 +142,13 @@ __device__ __forceinline__ float rng_uniform(uint64_t seed, uint64_t offset, uin
 
 constexpr int STAGE_SLOTS = 4;  // chunk pairs a thread can stage for the gather
 
+// Wide selection (k > 256 on split rows): candidates ranked by key bins d = M - key below the
+// slice maximum M.  A bin holding more than WIDE_BIN_MAX candidates (heavy ties, where the
+// in-bin ranking is quadratic) or a bound farther than WIDE_BINS keys below M sends the
+// slice to the general selection.
+constexpr int WIDE_BINS = 1024;
+constexpr int WIDE_BIN_MAX = 256;
+
 template <int NT>
 struct Smem {
   union {
@@ -159,6 +166,10 @@ struct Smem {
       uint32_t suf[256];          // suffix sums of the folded histogram
     } rx;
     uint32_t lb[1024];            // per-wave sorted thread maxima (lower bound)
+    struct {
+      uint32_t hist[WIDE_BINS];   // bin counts, then bin ends (bin d: key M - d)
+      uint32_t fill[WIDE_BINS];   // candidates per bin
+    } wb;
   } u;
   int32_t wsum[2][16];         // per-wave partials for block scans (double-buffered)
   int32_t misc[16];
@@ -256,6 +267,97 @@ __device__ __forceinline__ void find_bucket(const uint32_t* suf, int want, int a
       *out_bucket = b;
       *out_above = above_base + (int)next;
     }
+  }
+}
+
+// The first bin b of h[0..NB) at which the running sum h[0] + ... + h[b] reaches `want`, or -1
+// when the whole histogram holds fewer (uniform).  NB / NT consecutive bins per thread, one
+// block scan; wsum is the scan's per-wave buffer, *out a word of LDS for the answer.
+template <int NT, int NB>
+__device__ __forceinline__ int block_first_reach(const uint32_t* h, uint32_t want, int32_t* wsum,
+                                                 int32_t* out) {
+  constexpr int PER = NB / NT > 0 ? NB / NT : 1;
+  const int b0 = (int)threadIdx.x * PER;
+  uint32_t loc[PER];
+  uint32_t s = 0;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    loc[j] = b0 + j < NB ? h[b0 + j] : 0u;
+    s += loc[j];
+  }
+  int total = 0;
+  uint32_t run = (uint32_t)block_excl_scan<NT>((int)s, &total, wsum);
+  if ((uint32_t)total < want) return -1;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    if (run < want && run + loc[j] >= want) *out = b0 + j;
+    run += loc[j];
+  }
+  __syncthreads();
+  return __builtin_amdgcn_readfirstlane(*out);
+}
+
+// h[b] <- exclusive prefix of cnt[0..NB) at b (bin starts); returns the total (uniform) and
+// sets *big when a bin holds more than `cap` (uniform after the closing barrier).
+template <int NT, int NB>
+__device__ __forceinline__ int block_bin_starts(const uint32_t* cnt, uint32_t* h, uint32_t cap,
+                                                int32_t* wsum, bool* big) {
+  constexpr int PER = NB / NT > 0 ? NB / NT : 1;
+  const int b0 = (int)threadIdx.x * PER;
+  uint32_t loc[PER];
+  uint32_t s = 0;
+  bool over = false;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    loc[j] = b0 + j < NB ? cnt[b0 + j] : 0u;
+    s += loc[j];
+    over |= loc[j] > cap;
+  }
+  int total = 0;
+  uint32_t run = (uint32_t)block_excl_scan<NT>((int)s, &total, wsum);
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    if (b0 + j < NB) h[b0 + j] = run;
+    run += loc[j];
+  }
+  *big = __syncthreads_or(over ? 1 : 0) != 0;
+  return total;
+}
+
+// Output r of the descending merge of two descending lists a[0..K), b[0..K) of unique words
+// (zero words pad a short list and sort last): i, the number of a-words among the first r
+// outputs, is the first index of the diagonal i + j = r - 1 where a[i] > b[r - 1 - i] fails
+// (the predicate only turns from true to false along it), and output r is the larger of
+// a[i] and b[r - i].
+__device__ __forceinline__ uint64_t merge_path_at(const uint64_t* a, const uint64_t* b, int K,
+                                                  int r) {
+  int lo = r - K > 0 ? r - K : 0;
+  int hi = r < K ? r : K;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (a[mid] > b[r - 1 - mid]) lo = mid + 1;
+    else hi = mid;
+  }
+  const uint64_t x = lo < K ? a[lo] : 0ull;
+  const uint64_t y = r - lo < K ? b[r - lo] : 0ull;
+  return x > y ? x : y;
+}
+
+// Words grouped by bin in a[0..n) (bin d at [end[d] - cnt[d], end[d]), d = M - key): each word's
+// rank in descending word order is its bin's start plus the words of its bin above it; the
+// ranks below `keep` are written to out[].  Words are unique, so the ranks are a permutation.
+template <int NT>
+__device__ __forceinline__ void block_rank_bins(const uint64_t* a, int n, uint32_t M,
+                                                const uint32_t* end, const uint32_t* cnt,
+                                                int keep, uint64_t* out) {
+  for (int i = threadIdx.x; i < n; i += NT) {
+    const uint64_t w = a[i];
+    const uint32_t d = M - (uint32_t)(w >> 32);
+    const int e = (int)end[d];
+    const int b = e - (int)cnt[d];
+    int r = b;
+    for (int j = b; j < e; ++j) r += a[j] > w ? 1 : 0;
+    if (r < keep) out[r] = w;
   }
 }
 
@@ -1042,6 +1144,8 @@ __device__ __forceinline__ void static_for(F&& f) {
 
 template <int NT, int CH, bool VEC, bool MERGE>
 __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
+  static_assert(NT < 512 || sizeof(Smem<NT>::g) >= 2 * CAND_CAP * sizeof(uint64_t),
+                "the wide merge keeps the lists and their binned copy in g");
   constexpr int W = NT / 64;                 // waves per workgroup
   constexpr int NP = (CH + 1) / 2;           // chunk pairs
   __shared__ Smem<NT> sm;
@@ -1562,6 +1666,86 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
     return;
   }
 
+  // Wide selection (k > 256, split rows, the MERGE instantiations of 512 threads and more):
+  // the slice's top keff sorted into top[] by counting instead of comparison networks.
+  //   a. M = the slice maximum; histogram of the 8-element group maxima (the halves of the
+  //      pair maxima pm[]) over bins d = M - g < WIDE_BINS;
+  //   b. L = M - d*, d* the first bin where the running count reaches keff: at least keff
+  //      groups, so at least keff elements, are >= L (a valid lower bound, ~1.1k candidates
+  //      at k = 1024 on the C4 rows);
+  //   c. count the elements >= L per bin, bin starts by one block scan;
+  //   d. scatter their (key, ~id) words into their bins (an LDS atomic per word);
+  //   e. rank each word inside its bin (the bin's other words above it) -- its rank in the
+  //      slice -- and write ranks < keff to top[].
+  // Six barriers and O(1) work per candidate, where the general path runs radix passes over
+  // the registers and a bitonic sort.  Returns false (uniform) when the bound is farther than
+  // WIDE_BINS keys below M, the candidates overflow cand[], or a bin exceeds WIDE_BIN_MAX:
+  // the general path then runs from the start (nothing it reads has been changed).
+  auto wide_select = [&](uint32_t tm) -> bool {
+    uint32_t* hist = sm.u.wb.hist;
+    uint32_t* fill = sm.u.wb.fill;
+    uint64_t* cbuf = sm.g.cand;
+    for (int i = t; i < WIDE_BINS; i += NT) {
+      hist[i] = 0u;
+      fill[i] = 0u;
+    }
+    const uint32_t wm = wave_max_u32(tm);
+    if (lane == 0) sm.wsum[0][wid] = (int)wm;
+    __syncthreads();
+    uint32_t M = 0;
+#pragma unroll
+    for (int w = 0; w < W; ++w) M = max(M, (uint32_t)sm.wsum[0][w]);
+    M = __builtin_amdgcn_readfirstlane(M);
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      const uint32_t g0 = pm[i] & 0xFFFFu, g1 = pm[i] >> 16;
+      if (g0 != 0u && M - g0 < (uint32_t)WIDE_BINS) atomicAdd(&hist[M - g0], 1u);
+      if (g1 != 0u && M - g1 < (uint32_t)WIDE_BINS) atomicAdd(&hist[M - g1], 1u);
+    }
+    __syncthreads();
+    FSAMP_TRACE(2);
+    const int dstar = block_first_reach<NT, WIDE_BINS>(hist, (uint32_t)keff, sm.wsum[1],
+                                                       &sm.misc[M_LB]);
+    if (dstar < 0) return false;
+    const uint32_t L = M - (uint32_t)dstar;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      if (pair_ge(c, L)) {
+        uint32_t m = ge_mask(kv[c], L);
+        while (m != 0u) {
+          const int j = __ffs(m) - 1;
+          m &= m - 1u;
+          atomicAdd(&fill[M - key_at(kv[c], j)], 1u);
+        }
+      }
+    }
+    __syncthreads();
+    FSAMP_TRACE(3);
+    bool big = false;
+    const int n = block_bin_starts<NT, WIDE_BINS>(fill, hist, (uint32_t)WIDE_BIN_MAX, sm.wsum[0],
+                                                  &big);
+    if (big || n > CAND_CAP) return false;
+    const uint32_t idb = opaque_base(lo, t);
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      if (pair_ge(c, L)) {
+        uint32_t m = ge_mask(kv[c], L);
+        const uint32_t id0 = idb + (uint32_t)(c * NT * 8);
+        while (m != 0u) {
+          const int j = __ffs(m) - 1;
+          m &= m - 1u;
+          const uint32_t key = key_at(kv[c], j);
+          cbuf[atomicAdd(&hist[M - key], 1u)] = pack(key, id0 + (uint32_t)j);
+        }
+      }
+    }
+    __syncthreads();
+    FSAMP_TRACE(4);
+    block_rank_bins<NT>(cbuf, n, M, hist, fill, keff, sm.top);
+    __syncthreads();
+    return true;
+  };
+
   // Single-phase selection: L from every thread maximum, one gather, and the exact radix
   // select when the candidates overflow.
   int ncand = 0;
@@ -1569,7 +1753,15 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
   uint32_t L_sel = 1u;
   bool sorted_in_lds = false;
   bool regions = true;  // candidates in per-wave regions of top[] (else contiguous in cand[])
-  if (keff > 0) {
+  bool wide_done = false;
+  if constexpr (MERGE && NT >= 512) {
+    if (keff > 256 && p.S > 1 && p.stop >= 4) wide_done = wide_select(tmax);
+  }
+  if (wide_done) {
+    ncand = keff;
+    sorted_in_lds = true;
+    regions = false;
+  } else if (keff > 0) {
     const uint32_t L = lower_bound(tmax);
     if (p.stop == 2) {
       if (t == 0 && split == 0) p.out[row] = (int64_t)L;
@@ -1767,6 +1959,7 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
     // the S lists into cand[], four agent-scope loads in flight per thread
     const int n = p.S * p.K;
     const uint64_t* src = p.partials + (size_t)row * p.S * p.K;
+    constexpr bool WIDE_MERGE = NT >= 512;
     for (int i0 = 0; i0 < n; i0 += 4 * NT) {
       uint64_t w4[4];
   #pragma unroll
@@ -1783,21 +1976,52 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
     }
     __syncthreads();
     FSAMP_TRACE(7);
-    // top[0..P) runs the merged list (zeros past it); each further list, reversed, is folded
-    // in by an elementwise maximum (a bitonic sequence holding the top P of both) and a merge
-    int P = 64;
-    while (P < p.K) P <<= 1;
-    for (int i = t; i < P; i += NT) sm.top[i] = i < p.K ? sm.g.cand[i] : 0ull;
-    __syncthreads();
-    for (int sl = 1; sl < p.S; ++sl) {
-      for (int i = t; i < P; i += NT) {
-        const int e = P - 1 - i;
-        const uint64_t b = e < p.K ? sm.g.cand[sl * p.K + e] : 0ull;
-        const uint64_t a = sm.top[i];
-        sm.top[i] = a > b ? a : b;
+    // Wide lists: pairwise merges of the sorted lists, each output word placed by its
+    // merge-path split (a binary search over the pair's diagonal), in ceil(log2 S) rounds with
+    // a barrier each; the last round writes top[].  Lists ping-pong between cand[] and the
+    // second half of g.
+    bool ranked = false;
+    if constexpr (WIDE_MERGE) {
+      if (p.K > 256) {
+        const int K = p.K;
+        uint64_t* gw = reinterpret_cast<uint64_t*>(&sm.g);  // cand[] is its first CAND_CAP words
+        int nl = p.S, cur = 0;
+        while (nl > 1) {
+          const int np = nl >> 1;
+          const uint64_t* src = gw + cur * CAND_CAP;
+          uint64_t* dst = nl == 2 ? sm.top : gw + (cur ^ 1) * CAND_CAP;
+          for (int q = 0; q < np; ++q) {
+            const uint64_t* a = src + (size_t)(2 * q) * K;
+            const uint64_t* b = a + K;
+            for (int r = t; r < K; r += NT) dst[q * K + r] = merge_path_at(a, b, K, r);
+          }
+          if (nl & 1)
+            for (int r = t; r < K; r += NT) dst[np * K + r] = src[(nl - 1) * K + r];
+          __syncthreads();
+          nl = np + (nl & 1);
+          cur ^= 1;
+        }
+        ranked = true;
       }
+    }
+    if (!ranked) {
+      // top[0..P) runs the merged list (zeros past it); each further list, reversed, is
+      // folded in by an elementwise maximum (a bitonic sequence holding the top P of both)
+      // and a merge
+      int P = 64;
+      while (P < p.K) P <<= 1;
+      for (int i = t; i < P; i += NT) sm.top[i] = i < p.K ? sm.g.cand[i] : 0ull;
       __syncthreads();
-      block_bitonic_merge_desc<NT>(sm.top, P);
+      for (int sl = 1; sl < p.S; ++sl) {
+        for (int i = t; i < P; i += NT) {
+          const int e = P - 1 - i;
+          const uint64_t b = e < p.K ? sm.g.cand[sl * p.K + e] : 0ull;
+          const uint64_t a = sm.top[i];
+          sm.top[i] = a > b ? a : b;
+        }
+        __syncthreads();
+        block_bitonic_merge_desc<NT>(sm.top, P);
+      }
     }
     FSAMP_TRACE(8);
     merged = true;

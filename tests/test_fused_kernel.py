@@ -190,6 +190,33 @@ def test_split_rows_with_wide_k_merge_in_the_workgroup_exactly(k):
         assert np.array_equal(ren.view(np.uint32), want.renormed.view(np.uint32)), s
 
 
+@pytest.mark.parametrize("k", [300, 1000])
+def test_wide_selection_falls_back_where_its_key_bins_do_not_reach(k):
+    # Split rows with k > 256 rank their candidates in key bins below the slice maximum and
+    # merge the lists the same way.  Row 0: split 0 holds 100 values near +8 and otherwise
+    # -1e4, the other splits values near -50 -- split 0's bound lies past the bins (its slice
+    # falls back to the general selection) and the merged top k mostly lies past the bins of
+    # the row maximum (the merge falls back to the bitonic merge).  Row 1: values spread over
+    # many binades (the bound lies past the bins in every slice).  Row 2: ordinary values.
+    B, V = 3, 151936
+    g = np.random.Generator(np.random.PCG64(4100 + k))
+    x32 = np.empty((B, V), np.float32)
+    x32[0] = -50.0 + g.standard_normal(V)
+    x32[0, :V // 4] = -1.0e4 + g.standard_normal(V // 4)
+    x32[0, :100] = 8.0 + g.standard_normal(100)
+    x32[1] = np.sign(g.standard_normal(V)) * np.exp2(g.uniform(-60.0, 60.0, V))
+    x32[2] = 3.0 * g.standard_normal(V)
+    bits = W.to_bits(x32, "bfloat16")
+    x = dev(bits, "bfloat16")
+    u = ustream(B, 4200 + k)
+    want = oracle(bits, "bfloat16", k, 0.99, u)
+    for s in (0, 4):
+        tok, _, keep, ren = run_u(x, k, 0.99, u, s)
+        assert np.array_equal(fused_sampling.topk_fused(x, k, s).cpu().numpy(), want.topk_ids), s
+        assert np.array_equal(tok, want.token_ids), s
+        assert np.array_equal(ren.view(np.uint32), want.renormed.view(np.uint32)), s
+
+
 def test_vocabularies_past_18_bit_ids_keep_the_exact_order():
     # ids of 2^18 and more do not fit the 32-bit sort words: those slices sort 64-bit words
     V = (1 << 18) + 4000
