@@ -142,10 +142,16 @@ __device__ __forceinline__ float rng_uniform(uint64_t seed, uint64_t offset, uin
 
 constexpr int STAGE_SLOTS = 4;  // chunk pairs a thread can stage for the gather
 
-// Wide selection (k > 256 on split rows): candidates ranked by key bins d = M - key below the
-// slice maximum M.  A bin holding more than WIDE_BIN_MAX candidates (heavy ties, where the
-// in-bin ranking is quadratic) or a bound farther than WIDE_BINS keys below M sends the
-// slice to the general selection.
+// Wide selection (k > WIDE_MIN on split rows): candidates ranked by key bins d = M - key
+// below the slice maximum M.  A bin holding more than WIDE_BIN_MAX candidates (heavy ties,
+// where the in-bin ranking is quadratic) or a bound farther than WIDE_BINS keys below M sends
+// the slice to the general selection.  On split rows with k = 256 it measured 18.2 us against
+// 22.3 us for the general selection and bitonic merge (B=16, V=151936, six splits).
+#ifdef FSAMP_WIDE_MIN
+constexpr int WIDE_MIN = FSAMP_WIDE_MIN;
+#else
+constexpr int WIDE_MIN = 128;    // the wide selection and merge serve k > WIDE_MIN
+#endif
 constexpr int WIDE_BINS = 1024;
 constexpr int WIDE_BIN_MAX = 256;
 
@@ -1666,7 +1672,7 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
     return;
   }
 
-  // Wide selection (k > 256, split rows, the MERGE instantiations of 512 threads and more):
+  // Wide selection (k > WIDE_MIN, split rows, the MERGE instantiations of 512 threads and up):
   // the slice's top keff sorted into top[] by counting instead of comparison networks.
   //   a. M = the slice maximum; histogram of the 8-element group maxima (the halves of the
   //      pair maxima pm[]) over bins d = M - g < WIDE_BINS;
@@ -1755,7 +1761,7 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
   bool regions = true;  // candidates in per-wave regions of top[] (else contiguous in cand[])
   bool wide_done = false;
   if constexpr (MERGE && NT >= 512) {
-    if (keff > 256 && p.S > 1 && p.stop >= 4) wide_done = wide_select(tmax);
+    if (keff > WIDE_MIN && p.S > 1 && p.stop >= 4) wide_done = wide_select(tmax);
   }
   if (wide_done) {
     ncand = keff;
@@ -1982,7 +1988,7 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
     // second half of g.
     bool ranked = false;
     if constexpr (WIDE_MERGE) {
-      if (p.K > 256) {
+      if (p.K > WIDE_MIN) {
         const int K = p.K;
         uint64_t* gw = reinterpret_cast<uint64_t*>(&sm.g);  // cand[] is its first CAND_CAP words
         int nl = p.S, cur = 0;
