@@ -665,7 +665,9 @@ __device__ __forceinline__ void sample_tail(const Params& p, const uint64_t (&v)
   const int K = rc.k;
   const float u = rc.u;
   const int l = lane_id();
-  const int R = (K + 63) >> 6;
+  // ranks per lane; a compile-time 1 for RB = 1 (K <= 64), so that the lane of rank r is r
+  // itself rather than an integer division on the draw's critical path
+  const int R = RB == 1 ? 1 : (K + 63) >> 6;
   const int base = l * R;
   auto word = [&](int j) -> uint64_t {
     if constexpr (FROM_LDS) return top[base + j];
@@ -777,7 +779,7 @@ __device__ __forceinline__ void wave_finish(const Params& p, uint64_t (&v)[RB], 
     return;
   }
   advance_offset(p);
-  const int R = (rc.k + 63) >> 6;
+  const int R = RB == 1 ? 1 : (rc.k + 63) >> 6;  // rc.k <= p.K <= 64 when RB = 1
   if (R != RB) {
 #pragma unroll
     for (int i = 0; i < RB; ++i) {
