@@ -212,15 +212,10 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
   return max(v, xor_lane<32>(v));
 }
 
-// inclusive prefix over the 64 lanes (integers: the association does not matter)
+// inclusive prefix over the 64 lanes (integers: the association does not matter), by the
+// DPP row shifts and row broadcasts of wave_incl_scan_u32 (no LDS round trips)
 __device__ __forceinline__ int wave_incl_scan_i32(int v) {
-  const int lane = lane_id();
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int o = __shfl_up(v, d, 64);
-    if (lane >= d) v += o;
-  }
-  return v;
+  return (int)wave_incl_scan_u32((uint32_t)v);
 }
 
 // Exclusive prefix of v over the workgroup in thread order; *total gets the sum.
@@ -362,7 +357,12 @@ __device__ __forceinline__ void block_rank_bins(const uint64_t* a, int n, uint32
     const int e = (int)end[d];
     const int b = e - (int)cnt[d];
     int r = b;
-    for (int j = b; j < e; ++j) r += a[j] > w ? 1 : 0;
+    int j = b;
+    for (; j + 4 <= e; j += 4) {  // four independent reads in flight per step
+      const uint64_t a0 = a[j], a1 = a[j + 1], a2 = a[j + 2], a3 = a[j + 3];
+      r += (a0 > w ? 1 : 0) + (a1 > w ? 1 : 0) + (a2 > w ? 1 : 0) + (a3 > w ? 1 : 0);
+    }
+    for (; j < e; ++j) r += a[j] > w ? 1 : 0;
     if (r < keep) out[r] = w;
   }
 }
@@ -1681,14 +1681,16 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
   //   b. L = M - d*, d* the first bin where the running count reaches keff: at least keff
   //      groups, so at least keff elements, are >= L (a valid lower bound, ~1.1k candidates
   //      at k = 1024 on the C4 rows);
-  //   c. count the elements >= L per bin, bin starts by one block scan;
-  //   d. scatter their (key, ~id) words into their bins (an LDS atomic per word);
+  //   c. gather the elements >= L as (key, ~id) words (one register pass, wave slots from one
+  //      LDS atomic), counting them per bin; bin starts by one block scan;
+  //   d. scatter the words into their bins (an LDS atomic per word);
   //   e. rank each word inside its bin (the bin's other words above it) -- its rank in the
   //      slice -- and write ranks < keff to top[].
-  // Six barriers and O(1) work per candidate, where the general path runs radix passes over
-  // the registers and a bitonic sort.  Returns false (uniform) when the bound is farther than
-  // WIDE_BINS keys below M, the candidates overflow cand[], or a bin exceeds WIDE_BIN_MAX:
-  // the general path then runs from the start (nothing it reads has been changed).
+  // Nine barriers, one register pass after the bound and O(1) LDS work per candidate, where
+  // the general path runs radix passes over the registers and a bitonic sort.  Returns false
+  // (uniform) when the bound is farther than WIDE_BINS keys below M, the candidates overflow
+  // CAND_CAP, or a bin exceeds WIDE_BIN_MAX: the general path then runs from the start (the
+  // candidate counter is cleared again; nothing else it reads has been changed).
   auto wide_select = [&](uint32_t tm) -> bool {
     uint32_t* hist = sm.u.wb.hist;
     uint32_t* fill = sm.u.wb.fill;
@@ -1716,23 +1718,17 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
                                                        &sm.misc[M_LB]);
     if (dstar < 0) return false;
     const uint32_t L = M - (uint32_t)dstar;
+    // one pass over the registers: the words >= L into comp[] (slots per wave from one LDS
+    // atomic, the lanes' offsets from a DPP scan of their counts), counted per bin
+    uint64_t* comp = reinterpret_cast<uint64_t*>(&sm.g) + CAND_CAP;
+    uint32_t mine = 0;
 #pragma unroll
-    for (int c = 0; c < CH; ++c) {
-      if (pair_ge(c, L)) {
-        uint32_t m = ge_mask(kv[c], L);
-        while (m != 0u) {
-          const int j = __ffs(m) - 1;
-          m &= m - 1u;
-          atomicAdd(&fill[M - key_at(kv[c], j)], 1u);
-        }
-      }
-    }
-    __syncthreads();
-    FSAMP_TRACE(3);
-    bool big = false;
-    const int n = block_bin_starts<NT, WIDE_BINS>(fill, hist, (uint32_t)WIDE_BIN_MAX, sm.wsum[0],
-                                                  &big);
-    if (big || n > CAND_CAP) return false;
+    for (int c = 0; c < CH; ++c)
+      if (pair_ge(c, L)) mine += (uint32_t)__popc(ge_mask(kv[c], L));
+    const uint32_t incl = wave_incl_scan_u32(mine);
+    int wbase = 0;
+    if (lane == 63) wbase = atomicAdd(&sm.misc[M_CNT], (int)incl);
+    int slot = __builtin_amdgcn_readlane(wbase, 63) + (int)(incl - mine);
     const uint32_t idb = opaque_base(lo, t);
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
@@ -1743,9 +1739,27 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
           const int j = __ffs(m) - 1;
           m &= m - 1u;
           const uint32_t key = key_at(kv[c], j);
-          cbuf[atomicAdd(&hist[M - key], 1u)] = pack(key, id0 + (uint32_t)j);
+          atomicAdd(&fill[M - key], 1u);
+          if (slot < CAND_CAP) comp[slot] = pack(key, id0 + (uint32_t)j);
+          ++slot;
         }
       }
+    }
+    __syncthreads();
+    FSAMP_TRACE(3);
+    const int n = __builtin_amdgcn_readfirstlane(sm.misc[M_CNT]);
+    bool big = false;
+    block_bin_starts<NT, WIDE_BINS>(fill, hist, (uint32_t)WIDE_BIN_MAX, sm.wsum[0], &big);
+    if (big || n > CAND_CAP) {
+      // every thread read the count before the bin scan's barriers: clear it for the general
+      // selection's gather
+      if (t == 0) sm.misc[M_CNT] = 0;
+      return false;
+    }
+    // the words into their bins
+    for (int i = t; i < n; i += NT) {
+      const uint64_t w = comp[i];
+      cbuf[atomicAdd(&hist[M - (uint32_t)(w >> 32)], 1u)] = w;
     }
     __syncthreads();
     FSAMP_TRACE(4);
