@@ -659,9 +659,12 @@ __device__ __forceinline__ void advance_offset(const Params& p) {
   }
 }
 
+// wpre (FROM_LDS only, or nullptr): the unnormalised weights exp((x_i - m) * inv_t) of every
+// rank i < rc.k, already computed by the whole workgroup with the same operations.
 template <int RB, bool FROM_LDS>
 __device__ __forceinline__ void sample_tail(const Params& p, const uint64_t (&v)[RB],
-                                            const uint64_t* top, const RowCtl& rc, int row) {
+                                            const uint64_t* top, const RowCtl& rc, int row,
+                                            const float* wpre = nullptr) {
   const int K = rc.k;
   const float u = rc.u;
   const int l = lane_id();
@@ -682,8 +685,13 @@ __device__ __forceinline__ void sample_tail(const Params& p, const uint64_t (&v)
 #pragma unroll
   for (int j = 0; j < RB; ++j) {
     const bool valid = j < R && base + j < K;
-    const float x = key_to_float((uint32_t)(word(j) >> 32), p.is_bf16);
-    const float e = exp_nonpos((x - m) * rc.inv_t);
+    float e;
+    if (FROM_LDS && wpre != nullptr) {
+      e = wpre[base + j];
+    } else {
+      const float x = key_to_float((uint32_t)(word(j) >> 32), p.is_bf16);
+      e = exp_nonpos((x - m) * rc.inv_t);
+    }
     w[j] = valid ? e : 0.0f;
     s = s + w[j];
   }
@@ -890,7 +898,8 @@ __device__ __forceinline__ uint32_t key_of16(uint32_t w0, uint32_t w1, uint32_t 
 template <int RB, int NT>
 __device__ __forceinline__ void wave_back_wide(const Params& p, Smem<NT>& sm, int keff, int ncand,
                                                bool sorted_in_lds, bool regions, int row,
-                                               int split, const RowCtl& rc, int S);
+                                               int split, const RowCtl& rc, int S,
+                                               const float* wpre);
 
 template <int RB, int NT>
 __device__ __forceinline__ void wave_tail_regs(const Params& p, Smem<NT>& sm, uint64_t (&v)[RB],
@@ -938,9 +947,9 @@ __device__ __forceinline__ uint64_t wave_top64_of128(uint64_t a, uint64_t b, uin
 template <int RB, int NT>
 __device__ __forceinline__ void wave_back(const Params& p, Smem<NT>& sm, int keff, int ncand, bool sorted_in_lds,
                           bool regions, int row, int split, const RowCtl& rc, uint32_t L,
-                          uint64_t pre, int S) {
+                          uint64_t pre, int S, const float* wpre = nullptr) {
   if constexpr (RB > 4) {
-    wave_back_wide<RB, NT>(p, sm, keff, ncand, sorted_in_lds, regions, row, split, rc, S);
+    wave_back_wide<RB, NT>(p, sm, keff, ncand, sorted_in_lds, regions, row, split, rc, S, wpre);
     return;
   }
   const int l = lane_id();
@@ -1052,7 +1061,8 @@ __device__ __forceinline__ void wave_tail_regs(const Params& p, Smem<NT>& sm, ui
 template <int RB, int NT>
 __device__ __forceinline__ void wave_back_wide(const Params& p, Smem<NT>& sm, int keff, int ncand,
                                                bool sorted_in_lds, bool regions, int row,
-                                               int split, const RowCtl& rc, int S) {
+                                               int split, const RowCtl& rc, int S,
+                                               const float* wpre) {
   const int l = lane_id();
   if (keff > 0 && !sorted_in_lds) {
     const uint64_t* base = regions ? sm.top : sm.g.cand;
@@ -1110,7 +1120,7 @@ __device__ __forceinline__ void wave_back_wide(const Params& p, Smem<NT>& sm, in
   }
   advance_offset(p);
   const uint64_t none[RB] = {};
-  sample_tail<RB, true>(p, none, sm.top, rc, row);
+  sample_tail<RB, true>(p, none, sm.top, rc, row, wpre);
   FSAMP_TRACE(9);
   FSAMP_RTRACE(1);
 }
@@ -1154,6 +1164,8 @@ template <int NT, int CH, bool VEC, bool MERGE>
 __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
   static_assert(NT < 512 || sizeof(Smem<NT>::g) >= 2 * CAND_CAP * sizeof(uint64_t),
                 "the wide merge keeps the lists and their binned copy in g");
+  static_assert(sizeof(Smem<NT>::u) >= FSAMP_K_MAX * sizeof(float),
+                "the wide tail's weights fit in u");
   constexpr int W = NT / 64;                 // waves per workgroup
   constexpr int NP = (CH + 1) / 2;           // chunk pairs
   __shared__ Smem<NT> sm;
@@ -2049,6 +2061,23 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
     merged = true;
   }
 
+  // Wide sampling tails after the workgroup merge: the whole workgroup computes every rank's
+  // unnormalised weight exp((x_i - m) * inv_t) into LDS (the operations wave 0's tail would
+  // run, 16 per lane at k = 1024), so that wave 0 keeps only the serial sums, scans and draw.
+  const float* wpre = nullptr;
+  if constexpr (MERGE) {
+    if (merged && p.K > 256 && p.ids == nullptr && p.words == nullptr && p.stop == 7) {
+      const RowCtl rc0 = row_ctl();
+      float* wl = reinterpret_cast<float*>(&sm.u);  // K <= 1024 floats; u is free by now
+      const float m = key_to_float((uint32_t)(sm.top[0] >> 32), p.is_bf16);
+      for (int i = t; i < rc0.k; i += NT)
+        wl[i] = exp_nonpos((key_to_float((uint32_t)(sm.top[i] >> 32), p.is_bf16) - m) *
+                           rc0.inv_t);
+      __syncthreads();
+      wpre = wl;
+    }
+  }
+
   // From here on wave 0 carries the workgroup alone: no more workgroup barriers.
   if (wid != 0) return;
   const RowCtl rc = row_ctl();
@@ -2063,7 +2092,7 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
   auto back = [&](auto rbc) {
     constexpr int RB = decltype(rbc)::value;
     wave_back<RB, NT>(p, sm, keff_b, ncand, sorted_in_lds, regions, row, split, rc, L_sel, pre,
-                      s_b);
+                      s_b, wpre);
   };
   if (p.K <= 64) back(IC<1>{});
   else if (p.K <= 128) back(IC<2>{});
