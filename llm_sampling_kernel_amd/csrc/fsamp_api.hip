@@ -283,6 +283,9 @@ Call classic(const void* logits, int dtype, int64_t B, int64_t V, int64_t top_k,
   c.ws = ws;
   c.ws_bytes = ws_bytes;
   c.splits_override = splits_override;
+#ifdef FSAMP_TUNE_THREADS
+  c.force_threads = FSAMP_TUNE_THREADS;  // tuning builds only: the workgroup size of every call
+#endif
   return c;
 }
 

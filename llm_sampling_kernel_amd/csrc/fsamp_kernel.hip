@@ -277,7 +277,7 @@ __device__ __forceinline__ void find_bucket(const uint32_t* suf, int want, int a
 template <int NT, int NB>
 __device__ __forceinline__ int block_first_reach(const uint32_t* h, uint32_t want, int32_t* wsum,
                                                  int32_t* out) {
-  constexpr int PER = NB / NT > 0 ? NB / NT : 1;
+  constexpr int PER = (NB + NT - 1) / NT;
   const int b0 = (int)threadIdx.x * PER;
   uint32_t loc[PER];
   uint32_t s = 0;
@@ -303,7 +303,7 @@ __device__ __forceinline__ int block_first_reach(const uint32_t* h, uint32_t wan
 template <int NT, int NB>
 __device__ __forceinline__ int block_bin_starts(const uint32_t* cnt, uint32_t* h, uint32_t cap,
                                                 int32_t* wsum, bool* big) {
-  constexpr int PER = NB / NT > 0 ? NB / NT : 1;
+  constexpr int PER = (NB + NT - 1) / NT;
   const int b0 = (int)threadIdx.x * PER;
   uint32_t loc[PER];
   uint32_t s = 0;
@@ -1181,25 +1181,33 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
   const int keff = min(p.K, count);
   FSAMP_TRACE(0);
   FSAMP_RTRACE(0);
-  // The row's uniform, offset and controls are fetched now, so that their latency hides under
-  // the slice loads, and only read at the tail (row_ctl): a value consumed here would make the
-  // wave wait for its load before issuing the slice loads.  Every one is loaded
-  // unconditionally, an absent one from a zero word, so that no branch joins registers with
-  // loads pending on one side (which also makes the wave wait), and the index carries a zero
-  // the compiler cannot see through, so that the values stay in VGPRs (a load from a uniform
-  // address would be moved to SGPRs right where it is issued, which waits for it).
+  // The row's uniform, offset and controls are fetched early, so that their latency hides
+  // under the slice loads, and only read at the tail (row_ctl): a value consumed at once would
+  // make the wave wait for its load before issuing the slice loads.  Tilings that load the
+  // whole slice at once fetch them at kernel start; the pipelined (streaming) tilings fetch them
+  // right after their last slice load is issued, so that the eight VGPRs they occupy are not
+  // held while the slice fills the register file, and they land with the slice's last bytes.
+  // Every one is loaded unconditionally, an absent one from a zero word, so that no branch
+  // joins registers with loads pending on one side (which also makes the wave wait), and the
+  // index carries a zero the compiler cannot see through, so that the values stay in VGPRs (a
+  // load from a uniform address would be moved to SGPRs right where it is issued, which waits
+  // for it).
   const int vz = opaque_vzero();
   const uint64_t* zw = g_zero_words;
-  const float u_ld = (p.u != nullptr ? p.u + row : reinterpret_cast<const float*>(zw))[vz];
-  const uint64_t off_ld = __hip_atomic_load((p.offset_src != nullptr ? p.offset_src : zw) + vz,
-                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const uint64_t seed_ld = (p.seed_src != nullptr ? p.seed_src : zw)[vz];
-  const int32_t topk_ld =
-      (p.topk_row != nullptr ? p.topk_row + row : reinterpret_cast<const int32_t*>(zw))[vz];
-  const float topp_ld =
-      (p.topp_row != nullptr ? p.topp_row + row : reinterpret_cast<const float*>(zw))[vz];
-  const float temp_ld =
-      (p.temp_row != nullptr ? p.temp_row + row : reinterpret_cast<const float*>(zw))[vz];
+  float u_ld, topp_ld, temp_ld;
+  int32_t topk_ld;
+  uint64_t off_ld, seed_ld;
+  auto issue_ctl = [&]() {
+    u_ld = (p.u != nullptr ? p.u + row : reinterpret_cast<const float*>(zw))[vz];
+    off_ld = __hip_atomic_load((p.offset_src != nullptr ? p.offset_src : zw) + vz,
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    seed_ld = (p.seed_src != nullptr ? p.seed_src : zw)[vz];
+    topk_ld = (p.topk_row != nullptr ? p.topk_row + row : reinterpret_cast<const int32_t*>(zw))[vz];
+    topp_ld = (p.topp_row != nullptr ? p.topp_row + row : reinterpret_cast<const float*>(zw))[vz];
+    temp_ld = (p.temp_row != nullptr ? p.temp_row + row : reinterpret_cast<const float*>(zw))[vz];
+  };
+  constexpr bool CTL_LATE = pipe_depth<NT, CH, VEC>() > 0;
+  if constexpr (!CTL_LATE) issue_ctl();
   auto row_ctl = [&]() -> RowCtl {
     // (made opaque here, so that no arithmetic on them is hoisted next to their loads)
     float u_v = u_ld, topp_v = topp_ld, temp_v = temp_ld;
@@ -1508,11 +1516,11 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
     FSAMP_TRACE(12);
   };
 
-  // candidates >= L of chunk pair i into this wave's region (capacity REG): slots from a ballot
-  // and its mbcnt over the wave-uniform count; used for the last pair of the streaming path,
-  // whose data lands last (one compare and one scalar branch when the wave has no candidate)
-  constexpr int REG = FSAMP_K_MAX / W;
-  auto gather_pair = [&](auto ic, uint32_t L, int& wcnt, uint64_t* region) {
+  // candidates >= L of chunk pair i appended to top[] (capacity FSAMP_K_MAX; more are counted,
+  // not written) at slots from one LDS atomic per wave on *cnt; used for the last pair of the
+  // streaming path, whose data lands last (one compare and one scalar branch when the wave has
+  // no candidate)
+  auto gather_pair = [&](auto ic, uint32_t L, int32_t* cnt) {
     constexpr int i = decltype(ic)::value;
     constexpr int c0 = 2 * i, c1 = 2 * i + 1;
     const uint32_t lm1 = (L - 1u) * 0x10001u;
@@ -1523,10 +1531,17 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
       m = ge_mask(kv[c0], L);
       if constexpr (c1 < CH) m |= ge_mask(kv[c1], L) << 8;
     }
+    const uint32_t mine = (uint32_t)__popc(m);
+    const uint32_t incl = wave_incl_scan_u32(mine);
+    int base = 0;
+    if (lane == 63) base = atomicAdd(cnt, (int)incl);
+    int slot = __builtin_amdgcn_readlane(base, 63) + (int)(incl - mine);
     const uint32_t idb = opaque_base(lo, t);
+    // (a wave-uniform loop around a guarded body: with a per-lane loop the select tree below
+    // is folded into an address into the chunk pair, which moves the pair to scratch memory
+    // for the whole kernel -- as key_at's chain does)
     for (;;) {
-      const uint64_t act = __ballot(m != 0u);
-      if (act == 0ull) break;
+      if (__ballot(m != 0u) == 0ull) break;
       if (m != 0u) {
         const int j = __ffs(m) - 1;
         m &= m - 1u;
@@ -1535,14 +1550,11 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
           key = key_of16(kv[c0][0], kv[c0][1], kv[c0][2], kv[c0][3], kv[c1][0], kv[c1][1],
                          kv[c1][2], kv[c1][3], j);
         else
-          key = key_at(kv[c0], j);
+          key = key_of16(kv[c0][0], kv[c0][1], kv[c0][2], kv[c0][3], 0u, 0u, 0u, 0u, j);
         const uint32_t id = idb + (uint32_t)((c0 + (j >> 3)) * NT * 8 + (j & 7));
-        const int below = (int)__builtin_amdgcn_mbcnt_hi(
-            (uint32_t)(act >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)act, 0u));
-        const int slot = wcnt + below;
-        if (slot < REG) region[slot] = pack(key, id);
+        if (slot < FSAMP_K_MAX) sm.top[slot] = pack(key, id);
+        ++slot;
       }
-      wcnt += (int)__popcll(act);
     }
   };
 
@@ -1558,7 +1570,14 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
       load_chunk(c + PD);
     });
     static_for<PB + PD, PB + PD + PX>([&](auto cc) { load_chunk(decltype(cc)::value); });
+    if constexpr (PB + PD + PX >= CH) issue_ctl();  // the slice's last load is issued
     __builtin_amdgcn_sched_barrier(0);
+  };
+  // load c + PD + PX after chunk c is converted; the row controls after the slice's last load
+  auto stream_next_load = [&](auto cc) {
+    constexpr int c = decltype(cc)::value;
+    if constexpr (c + PD + PX < CH) load_chunk(c + PD + PX);
+    if constexpr (c + PD + PX == CH - 1) issue_ctl();
   };
   // the rest of the slice without a gather (ablation stops, wide k, fallback)
   auto stream_loads_tail = [&]() {
@@ -1567,7 +1586,7 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
       __builtin_amdgcn_sched_barrier(0);
       convert(c);
       __builtin_amdgcn_sched_barrier(0);
-      if constexpr (c + PD + PX < CH) load_chunk(c + PD + PX);
+      stream_next_load(cc);
     });
     FSAMP_WTRACE(pm[NP - 1]);
   };
@@ -1576,6 +1595,7 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
     if (count > 0) {
       stream_loads_head();
     } else {
+      issue_ctl();
 #pragma unroll
       for (int c = 0; c < CH; ++c) kv[c][0] = kv[c][1] = kv[c][2] = kv[c][3] = 0u;
 #pragma unroll
@@ -1594,15 +1614,17 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
         if (t == 0 && split == 0) p.out[row] = (int64_t)L;
         return;
       }
-      // Candidates go to per-wave regions of top[] (REG words each) at a wave-uniform count:
-      // the prefix's, staged through LDS while the last loads are in flight; the middle pairs'
-      // (staged one by one as each lands, gathered while the last pair is still in flight);
-      // then the last pair's straight from registers, the only gather after the last byte.
-      int wcnt = 0;
-      uint64_t* region = sm.top + wid * REG;
+      // Candidates are appended to top[] at slots from an LDS atomic on the candidate counter
+      // (zeroed at kernel start), one per wave and gather: the prefix's, staged through LDS
+      // while the last loads are in flight; the middle pairs' (staged one by one as each
+      // lands, gathered while the last pair is still in flight); then the last pair's straight
+      // from registers, the only gather after the last byte.  After the barrier the candidates
+      // are top[0, total): wave 0 reads them without compacting per-wave lists.
+      int32_t* cnt = &sm.misc[M_CNT];
+      int unused = 0;
       int nst = 0;
       stage(IC<0>{}, IC<PB / 2>{}, L, nst);
-      extract(IC<0>{}, IC<PB>{}, L, nst, region, REG, nullptr, wcnt);
+      extract(IC<0>{}, IC<PB>{}, L, nst, sm.top, FSAMP_K_MAX, cnt, unused);
       constexpr int LASTP = NP - 1;  // the last pair (chunk 2*LASTP, and 2*LASTP + 1 if < CH)
       int nst2 = 0;
       static_for<PB, CH>([&](auto cc) {
@@ -1610,48 +1632,26 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
         __builtin_amdgcn_sched_barrier(0);
         convert(c);
         __builtin_amdgcn_sched_barrier(0);
-        if constexpr (c + PD + PX < CH) load_chunk(c + PD + PX);
+        stream_next_load(cc);
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (((c & 1) == 1 || c == CH - 1) && c / 2 < LASTP)
           stage(IC<c / 2>{}, IC<c / 2 + 1>{}, L, nst2);
         if constexpr (c == 2 * LASTP - 1)  // every middle pair staged: gather them
-          extract(IC<PB>{}, IC<2 * LASTP>{}, L, nst2, region, REG, nullptr, wcnt);
+          extract(IC<PB>{}, IC<2 * LASTP>{}, L, nst2, sm.top, FSAMP_K_MAX, cnt, unused);
       });
       FSAMP_WTRACE(pm[NP - 1]);
-      gather_pair(IC<LASTP>{}, L, wcnt, region);
-      if (lane == 0) sm.wsum[0][wid] = wcnt;
+      gather_pair(IC<LASTP>{}, L, cnt);
       __syncthreads();
       FSAMP_TRACE(4);
-      int cend[W];  // inclusive prefix of the per-wave counts
-      int total = 0;
-      bool full = false;
-#pragma unroll
-      for (int w = 0; w < W; ++w) {
-        const int cw = __builtin_amdgcn_readfirstlane(sm.wsum[0][w]);
-        full = full || cw > REG;
-        total += cw;
-        cend[w] = total;
-      }
+      const int total = __builtin_amdgcn_readfirstlane(sm.misc[M_CNT]);
       if (p.stop == 3) {
         if (t == 0 && split == 0) p.out[row] = total;
         return;
       }
-      if (!full && total <= 128) {
+      if (total <= 128) {
         if (wid != 0) return;
-        // candidate e of the concatenated regions
-        auto cand = [&](int e) -> uint64_t {
-          if (e >= total) return 0ull;
-          int w = 0, base = 0;
-#pragma unroll
-          for (int r = 0; r + 1 < W; ++r) {
-            if (e >= cend[r]) {
-              w = r + 1;
-              base = cend[r];
-            }
-          }
-          return sm.top[w * REG + (e - base)];
-        };
         FSAMP_TRACE(14);
+        auto cand = [&](int e) -> uint64_t { return e < total ? sm.top[e] : 0ull; };
         uint64_t v[1];
         if (total <= 64) v[0] = wave_sort64_words(cand(lane), L, p.V);
         else v[0] = wave_top64_of128(cand(lane), cand(64 + lane), L, p.V);
@@ -1660,10 +1660,16 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
         wave_tail_regs<1, NT>(p, sm, v, keff, row, split, rc, p.S);
         return;
       }
-      // too many candidates for the register sort: the general selection, full bound.  Every
-      // wave has read the total before the counter is cleared for the general gather.
+      // Too many candidates for the register sort (heavy ties near the bound): the general
+      // selection with the bound of the whole slice, on the slice read again from memory.  The
+      // reload keeps the streamed chunks dead once gathered, so the registers they held are
+      // free for the sort and the tail of the common case.  Every wave has read the total
+      // before the counter is cleared for the general gather.
       __syncthreads();
       if (t == 0) sm.misc[M_CNT] = 0;
+      load_slice();
+#pragma unroll
+      for (int c = 0; c < CH; ++c) convert(c);
     } else {
       if (count > 0) stream_loads_tail();
       else

@@ -39,15 +39,15 @@ template <int J>
 __device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
   const int x = (int)v;
   if constexpr (J == 1) {
-    return (uint32_t)__builtin_amdgcn_mov_dpp(x, DPP_QUAD_XOR1, 0xF, 0xF, false);
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, x, DPP_QUAD_XOR1, 0xF, 0xF, true);
   } else if constexpr (J == 2) {
-    return (uint32_t)__builtin_amdgcn_mov_dpp(x, DPP_QUAD_XOR2, 0xF, 0xF, false);
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, x, DPP_QUAD_XOR2, 0xF, 0xF, true);
   } else if constexpr (J == 4) {
     const int up = __builtin_amdgcn_mov_dpp(x, DPP_ROW_SHL4, 0xF, 0xF, false);
     const int dn = __builtin_amdgcn_mov_dpp(x, DPP_ROW_SHR4, 0xF, 0xF, false);
     return (uint32_t)((lane_id() & 4) ? dn : up);
   } else if constexpr (J == 8) {
-    return (uint32_t)__builtin_amdgcn_mov_dpp(x, DPP_ROW_ROR8, 0xF, 0xF, false);
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, x, DPP_ROW_ROR8, 0xF, 0xF, true);
   } else if constexpr (J == 16) {
     // swap(v, v): result[0] (vdst) has the even 16-lane rows' values in the odd rows,
     // result[1] (vsrc) the odd rows' values in the even rows
@@ -102,16 +102,372 @@ __device__ __forceinline__ T bitonic_levels(T v) {
   return bitonic_merge_stages<K, K / 2, T, ASC>(v);
 }
 
+// ---- 32-bit networks in the flip form, one compare-exchange stage per asm block -------------
+//
+// Every block of a level is sorted the same way (descending: the lower lane keeps the larger
+// word, or ascending), so the lanes that keep the larger word of a stage are the lanes whose
+// bit b is clear, b the stage's bit: the first stage of level K pairs lane l with l ^ (K-1)
+// (b = log2(K/2)), the later ones with l ^ J (b = log2 J).  Partners come from DPP moves
+// folded into v_max/v_min (quad_perm, row_half_mirror, row_mirror, row_shl/shr:4, row_ror:8)
+// or from v_permlane16/32_swap.  For b >= 2 the keep-max lanes are whole 4-lane banks (b = 2,
+// 3) or 16-lane rows (b = 4, 5): v_max writes those lanes and v_min the others through the DPP
+// bank/row write masks, so the stage is two independent instructions and no select.  For
+// b < 2 a v_cndmask with a constant lane mask picks max or min.  Each block starts with the
+// two wait states a DPP read of a VGPR written by the previous VALU instruction needs.
+
+namespace flipnet {
+
+// keep-max lane masks for b = 0, 1 (lanes with bit b clear)
+constexpr uint64_t KEEP_B0 = 0x5555555555555555ull;
+constexpr uint64_t KEEP_B1 = 0x3333333333333333ull;
+
+// partner by quad_perm, keep-max lanes given by a 64-bit mask
+#define FSAMP_QSTAGE(QP)                                                                        \
+  template <bool ASC>                                                                           \
+  __device__ __forceinline__ uint32_t qstage_##QP(uint32_t v, uint64_t keep_max) {              \
+    uint32_t mx, mn, r;                                                                         \
+    asm("s_nop 1\n\t"                                                                  \
+                 "v_max_u32_dpp %1, %3, %3 " QPSTR_##QP " row_mask:0xf bank_mask:0xf\n\t"        \
+                 "v_min_u32_dpp %2, %3, %3 " QPSTR_##QP " row_mask:0xf bank_mask:0xf\n\t"        \
+                 "v_cndmask_b32_e64 %0, %2, %1, %4"                                             \
+                 : "=v"(r), "=&v"(mx), "=&v"(mn)                                                \
+                 : "v"(v), "s"(ASC ? ~keep_max : keep_max));                                    \
+    return r;                                                                                   \
+  }
+#define QPSTR_x1 "quad_perm:[1,0,3,2]"
+#define QPSTR_x2 "quad_perm:[2,3,0,1]"
+#define QPSTR_x3 "quad_perm:[3,2,1,0]"
+FSAMP_QSTAGE(x1)
+FSAMP_QSTAGE(x2)
+FSAMP_QSTAGE(x3)
+#undef FSAMP_QSTAGE
+
+// partner by one DPP pattern for every lane; MAXBANKS / MINBANKS are the bank write masks
+#define FSAMP_BSTAGE(NAME, CTL, MAXB, MINB)                                                     \
+  template <bool ASC>                                                                           \
+  __device__ __forceinline__ uint32_t NAME(uint32_t v) {                                        \
+    uint32_t r;                                                                                 \
+    if constexpr (!ASC)                                                                         \
+      asm("s_nop 1\n\t"                                                                \
+                   "v_max_u32_dpp %0, %1, %1 " CTL " row_mask:0xf bank_mask:" MAXB "\n\t"       \
+                   "v_min_u32_dpp %0, %1, %1 " CTL " row_mask:0xf bank_mask:" MINB              \
+                   : "=&v"(r) : "v"(v));                                                        \
+    else                                                                                        \
+      asm("s_nop 1\n\t"                                                                \
+                   "v_min_u32_dpp %0, %1, %1 " CTL " row_mask:0xf bank_mask:" MAXB "\n\t"       \
+                   "v_max_u32_dpp %0, %1, %1 " CTL " row_mask:0xf bank_mask:" MINB              \
+                   : "=&v"(r) : "v"(v));                                                        \
+    return r;                                                                                   \
+  }
+FSAMP_BSTAGE(flip8, "row_half_mirror", "0x5", "0xa")  // l ^ 7,  b = 2
+FSAMP_BSTAGE(flip16, "row_mirror", "0x3", "0xc")      // l ^ 15, b = 3
+FSAMP_BSTAGE(ror8, "row_ror:8", "0x3", "0xc")         // l ^ 8,  b = 3
+#undef FSAMP_BSTAGE
+
+// l ^ 4, b = 2: banks 0 and 2 take lane l + 4 (row_shl:4), banks 1 and 3 lane l - 4 (row_shr:4)
+template <bool ASC>
+__device__ __forceinline__ uint32_t x4(uint32_t v) {
+  uint32_t r;
+  if constexpr (!ASC)
+    asm("s_nop 1\n\t"
+                 "v_max_u32_dpp %0, %1, %1 row_shl:4 row_mask:0xf bank_mask:0x5\n\t"
+                 "v_min_u32_dpp %0, %1, %1 row_shr:4 row_mask:0xf bank_mask:0xa"
+                 : "=&v"(r) : "v"(v));
+  else
+    asm("s_nop 1\n\t"
+                 "v_min_u32_dpp %0, %1, %1 row_shl:4 row_mask:0xf bank_mask:0x5\n\t"
+                 "v_max_u32_dpp %0, %1, %1 row_shr:4 row_mask:0xf bank_mask:0xa"
+                 : "=&v"(r) : "v"(v));
+  return r;
+}
+
+// Partner words of a row-level stage (b = 4 or 5) in two registers, then the masked max/min:
+// `even` holds the partner of the rows in MAXROWS' pattern, `odd` of the others.
+#define FSAMP_ROWPAIR(MAXR, MINR)                                                               \
+  if constexpr (!ASC)                                                                           \
+    asm("s_nop 1\n\t"                                                                  \
+                 "v_max_u32_dpp %0, %1, %3 quad_perm:[0,1,2,3] row_mask:" MAXR " bank_mask:0xf\n\t" \
+                 "v_min_u32_dpp %0, %2, %3 quad_perm:[0,1,2,3] row_mask:" MINR " bank_mask:0xf"   \
+                 : "=&v"(r) : "v"(pa), "v"(pb), "v"(v));                                        \
+  else                                                                                          \
+    asm("s_nop 1\n\t"                                                                  \
+                 "v_min_u32_dpp %0, %1, %3 quad_perm:[0,1,2,3] row_mask:" MAXR " bank_mask:0xf\n\t" \
+                 "v_max_u32_dpp %0, %2, %3 quad_perm:[0,1,2,3] row_mask:" MINR " bank_mask:0xf"   \
+                 : "=&v"(r) : "v"(pa), "v"(pb), "v"(v));
+
+// l ^ 16, b = 4: after v_permlane16_swap of two copies, the second holds the odd rows' words in
+// the even rows (the partners of rows 0 and 2, which keep the max) and the first the even rows'
+// words in the odd rows
+template <bool ASC>
+__device__ __forceinline__ uint32_t x16(uint32_t v) {
+  uint32_t a = v, b = v, r;
+  asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+  const uint32_t pa = b, pb = a;
+  FSAMP_ROWPAIR("0x5", "0xa")
+  return r;
+}
+
+// l ^ 31, b = 4: row_mirror, then the l ^ 16 exchange of the mirrored words
+template <bool ASC>
+__device__ __forceinline__ uint32_t flip32(uint32_t v) {
+  uint32_t a, b, r;
+  asm("s_nop 1\n\t"
+               "v_mov_b32_dpp %0, %2 row_mirror row_mask:0xf bank_mask:0xf\n\t"
+               "v_mov_b32_dpp %1, %2 row_mirror row_mask:0xf bank_mask:0xf\n\t"
+               "s_nop 1\n\t"
+               "v_permlane16_swap_b32 %0, %1\n\t"
+               "s_nop 1"
+               : "=&v"(a), "=&v"(b) : "v"(v));
+  const uint32_t pa = b, pb = a;
+  FSAMP_ROWPAIR("0x5", "0xa")
+  return r;
+}
+
+// l ^ 32, b = 5: after v_permlane32_swap of two copies, the second holds the upper half's words
+// in the lower half (partners of rows 0 and 1, which keep the max), the first the lower half's
+// words in the upper half
+template <bool ASC>
+__device__ __forceinline__ uint32_t x32(uint32_t v) {
+  uint32_t a = v, b = v, r;
+  asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+  const uint32_t pa = b, pb = a;
+  FSAMP_ROWPAIR("0x3", "0xc")
+  return r;
+}
+
+// l ^ 63, b = 5: t = row_mirror(v); v_permlane32_swap of two copies of t gives rows
+// (t0, t1, t0, t1) and (t2, t3, t2, t3); s = (t2, t3, t0, t1) by row-masked moves; after
+// v_permlane16_swap of two copies of s they hold (t2, t2, t0, t0) and (t3, t3, t1, t1), so
+// rows 0 and 2 find their partner in the second, rows 1 and 3 in the first.
+template <bool ASC>
+__device__ __forceinline__ uint32_t flip64(uint32_t v) {
+  uint32_t x, y, s0, s1, r;
+  asm("s_nop 1\n\t"
+               "v_mov_b32_dpp %0, %4 row_mirror row_mask:0xf bank_mask:0xf\n\t"
+               "v_mov_b32_dpp %1, %4 row_mirror row_mask:0xf bank_mask:0xf\n\t"
+               "s_nop 1\n\t"
+               "v_permlane32_swap_b32 %0, %1\n\t"
+               "s_nop 1\n\t"
+               "v_mov_b32_dpp %2, %1 quad_perm:[0,1,2,3] row_mask:0x3 bank_mask:0xf\n\t"
+               "v_mov_b32_dpp %2, %0 quad_perm:[0,1,2,3] row_mask:0xc bank_mask:0xf\n\t"
+               "v_mov_b32_e32 %3, %2\n\t"
+               "s_nop 1\n\t"
+               "v_permlane16_swap_b32 %2, %3\n\t"
+               "s_nop 1"
+               : "=&v"(x), "=&v"(y), "=&v"(s0), "=&v"(s1) : "v"(v));
+  if constexpr (!ASC)
+    asm("v_max_u32_dpp %0, %2, %3 quad_perm:[0,1,2,3] row_mask:0x1 bank_mask:0xf\n\t"
+                 "v_max_u32_dpp %0, %1, %3 quad_perm:[0,1,2,3] row_mask:0x2 bank_mask:0xf\n\t"
+                 "v_min_u32_dpp %0, %2, %3 quad_perm:[0,1,2,3] row_mask:0x4 bank_mask:0xf\n\t"
+                 "v_min_u32_dpp %0, %1, %3 quad_perm:[0,1,2,3] row_mask:0x8 bank_mask:0xf"
+                 : "=&v"(r) : "v"(s0), "v"(s1), "v"(v));
+  else
+    asm("v_min_u32_dpp %0, %2, %3 quad_perm:[0,1,2,3] row_mask:0x1 bank_mask:0xf\n\t"
+                 "v_min_u32_dpp %0, %1, %3 quad_perm:[0,1,2,3] row_mask:0x2 bank_mask:0xf\n\t"
+                 "v_max_u32_dpp %0, %2, %3 quad_perm:[0,1,2,3] row_mask:0x4 bank_mask:0xf\n\t"
+                 "v_max_u32_dpp %0, %1, %3 quad_perm:[0,1,2,3] row_mask:0x8 bank_mask:0xf"
+                 : "=&v"(r) : "v"(s0), "v"(s1), "v"(v));
+  return r;
+}
+#undef FSAMP_ROWPAIR
+
+// half-cleaner stages J, J/2, ..., 1 of one level
+template <int J, bool ASC>
+__device__ __forceinline__ uint32_t clean(uint32_t v) {
+  if constexpr (J == 32) v = x32<ASC>(v);
+  if constexpr (J >= 16) v = x16<ASC>(v);
+  if constexpr (J >= 8) v = ror8<ASC>(v);
+  if constexpr (J >= 4) v = x4<ASC>(v);
+  if constexpr (J >= 2) v = qstage_x2<ASC>(v, KEEP_B1);
+  if constexpr (J >= 1) v = qstage_x1<ASC>(v, KEEP_B0);
+  return v;
+}
+
+// the full 64-lane sort: levels 2 .. 64, each a flip stage and the half-cleaners below it
+template <bool ASC>
+__device__ __forceinline__ uint32_t sort64(uint32_t v) {
+  v = qstage_x1<ASC>(v, KEEP_B0);                 // level 2 (the flip is l ^ 1)
+  v = qstage_x3<ASC>(v, KEEP_B1);                 // level 4
+  v = clean<1, ASC>(v);
+  v = flip8<ASC>(v);                              // level 8
+  v = clean<2, ASC>(v);
+  v = flip16<ASC>(v);                             // level 16
+  v = clean<4, ASC>(v);
+  v = flip32<ASC>(v);                             // level 32
+  v = clean<8, ASC>(v);
+  v = flip64<ASC>(v);                             // level 64
+  return clean<16, ASC>(v);
+}
+
+
+// ---- the two sorts of wave_top64_of_two in one chain of blocks: a descending and b ascending,
+// stage by stage, so that each block carries two independent compare-exchanges (the second
+// sort's comparators are the first's mirrored: where a keeps the max, b keeps the min)
+
+#define FSAMP_DQSTAGE(QP)                                                                        \
+  __device__ __forceinline__ void dq_##QP(uint32_t& a, uint32_t& b, uint64_t keep_max) {        \
+    uint32_t a1, a2, b1, b2, ra, rb;                                                             \
+    asm("s_nop 1\n\t"                                                                            \
+        "v_max_u32_dpp %2, %6, %6 " QPSTR_##QP " row_mask:0xf bank_mask:0xf\n\t"                  \
+        "v_min_u32_dpp %3, %6, %6 " QPSTR_##QP " row_mask:0xf bank_mask:0xf\n\t"                  \
+        "v_max_u32_dpp %4, %7, %7 " QPSTR_##QP " row_mask:0xf bank_mask:0xf\n\t"                  \
+        "v_min_u32_dpp %5, %7, %7 " QPSTR_##QP " row_mask:0xf bank_mask:0xf\n\t"                  \
+        "v_cndmask_b32_e64 %0, %3, %2, %8\n\t"                                                   \
+        "v_cndmask_b32_e64 %1, %4, %5, %8"                                                       \
+        : "=v"(ra), "=v"(rb), "=&v"(a1), "=&v"(a2), "=&v"(b1), "=&v"(b2)                         \
+        : "v"(a), "v"(b), "s"(keep_max));                                                        \
+    a = ra;                                                                                      \
+    b = rb;                                                                                      \
+  }
+FSAMP_DQSTAGE(x1)
+FSAMP_DQSTAGE(x2)
+FSAMP_DQSTAGE(x3)
+#undef FSAMP_DQSTAGE
+
+#define FSAMP_DBSTAGE(NAME, CTLMAX, CTLMIN, MAXB, MINB)                                          \
+  __device__ __forceinline__ void NAME(uint32_t& a, uint32_t& b) {                              \
+    uint32_t ra, rb;                                                                             \
+    asm("s_nop 1\n\t"                                                                            \
+        "v_max_u32_dpp %0, %2, %2 " CTLMAX " row_mask:0xf bank_mask:" MAXB "\n\t"                \
+        "v_min_u32_dpp %0, %2, %2 " CTLMIN " row_mask:0xf bank_mask:" MINB "\n\t"                \
+        "v_min_u32_dpp %1, %3, %3 " CTLMAX " row_mask:0xf bank_mask:" MAXB "\n\t"                \
+        "v_max_u32_dpp %1, %3, %3 " CTLMIN " row_mask:0xf bank_mask:" MINB                       \
+        : "=&v"(ra), "=&v"(rb) : "v"(a), "v"(b));                                                \
+    a = ra;                                                                                      \
+    b = rb;                                                                                      \
+  }
+FSAMP_DBSTAGE(d_flip8, "row_half_mirror", "row_half_mirror", "0x5", "0xa")
+FSAMP_DBSTAGE(d_flip16, "row_mirror", "row_mirror", "0x3", "0xc")
+FSAMP_DBSTAGE(d_ror8, "row_ror:8", "row_ror:8", "0x3", "0xc")
+FSAMP_DBSTAGE(d_x4, "row_shl:4", "row_shr:4", "0x5", "0xa")
+#undef FSAMP_DBSTAGE
+
+// row-level stages: partners of a in (pa for the keep-max rows, pb for the others), of b in
+// (qa, qb); a keeps the max in rows MAXR, b the min
+#define FSAMP_DROWPAIR(MAXR, MINR)                                                               \
+  asm("s_nop 1\n\t"                                                                              \
+      "v_max_u32_dpp %0, %2, %6 quad_perm:[0,1,2,3] row_mask:" MAXR " bank_mask:0xf\n\t"          \
+      "v_min_u32_dpp %0, %3, %6 quad_perm:[0,1,2,3] row_mask:" MINR " bank_mask:0xf\n\t"          \
+      "v_min_u32_dpp %1, %4, %7 quad_perm:[0,1,2,3] row_mask:" MAXR " bank_mask:0xf\n\t"          \
+      "v_max_u32_dpp %1, %5, %7 quad_perm:[0,1,2,3] row_mask:" MINR " bank_mask:0xf"              \
+      : "=&v"(ra), "=&v"(rb) : "v"(pa), "v"(pb), "v"(qa), "v"(qb), "v"(a), "v"(b));
+
+__device__ __forceinline__ void d_x16(uint32_t& a, uint32_t& b) {
+  uint32_t a0 = a, a1 = a, b0 = b, b1 = b, ra, rb;
+  asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\tv_permlane16_swap_b32 %2, %3\n\ts_nop 1"
+      : "+v"(a0), "+v"(a1), "+v"(b0), "+v"(b1));
+  const uint32_t pa = a1, pb = a0, qa = b1, qb = b0;
+  FSAMP_DROWPAIR("0x5", "0xa")
+  a = ra;
+  b = rb;
+}
+
+__device__ __forceinline__ void d_x32(uint32_t& a, uint32_t& b) {
+  uint32_t a0 = a, a1 = a, b0 = b, b1 = b, ra, rb;
+  asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\tv_permlane32_swap_b32 %2, %3\n\ts_nop 1"
+      : "+v"(a0), "+v"(a1), "+v"(b0), "+v"(b1));
+  const uint32_t pa = a1, pb = a0, qa = b1, qb = b0;
+  FSAMP_DROWPAIR("0x3", "0xc")
+  a = ra;
+  b = rb;
+}
+
+__device__ __forceinline__ void d_flip32(uint32_t& a, uint32_t& b) {
+  uint32_t a0, a1, b0, b1, ra, rb;
+  asm("s_nop 1\n\t"
+      "v_mov_b32_dpp %0, %4 row_mirror row_mask:0xf bank_mask:0xf\n\t"
+      "v_mov_b32_dpp %1, %4 row_mirror row_mask:0xf bank_mask:0xf\n\t"
+      "v_mov_b32_dpp %2, %5 row_mirror row_mask:0xf bank_mask:0xf\n\t"
+      "v_mov_b32_dpp %3, %5 row_mirror row_mask:0xf bank_mask:0xf\n\t"
+      "s_nop 1\n\t"
+      "v_permlane16_swap_b32 %0, %1\n\t"
+      "v_permlane16_swap_b32 %2, %3\n\t"
+      "s_nop 1"
+      : "=&v"(a0), "=&v"(a1), "=&v"(b0), "=&v"(b1) : "v"(a), "v"(b));
+  const uint32_t pa = a1, pb = a0, qa = b1, qb = b0;
+  FSAMP_DROWPAIR("0x5", "0xa")
+  a = ra;
+  b = rb;
+}
+#undef FSAMP_DROWPAIR
+
+// partner l ^ 63 of both (see flip64): rows 0 and 2 of the second register, rows 1 and 3 of
+// the first
+__device__ __forceinline__ void d_flip64(uint32_t& a, uint32_t& b) {
+  uint32_t x, y, s0, s1, u, w, t0, t1, ra, rb;
+  asm("s_nop 1\n\t"
+      "v_mov_b32_dpp %0, %8 row_mirror row_mask:0xf bank_mask:0xf\n\t"
+      "v_mov_b32_dpp %1, %8 row_mirror row_mask:0xf bank_mask:0xf\n\t"
+      "v_mov_b32_dpp %4, %9 row_mirror row_mask:0xf bank_mask:0xf\n\t"
+      "v_mov_b32_dpp %5, %9 row_mirror row_mask:0xf bank_mask:0xf\n\t"
+      "s_nop 1\n\t"
+      "v_permlane32_swap_b32 %0, %1\n\t"
+      "v_permlane32_swap_b32 %4, %5\n\t"
+      "s_nop 1\n\t"
+      "v_mov_b32_dpp %2, %1 quad_perm:[0,1,2,3] row_mask:0x3 bank_mask:0xf\n\t"
+      "v_mov_b32_dpp %2, %0 quad_perm:[0,1,2,3] row_mask:0xc bank_mask:0xf\n\t"
+      "v_mov_b32_dpp %6, %5 quad_perm:[0,1,2,3] row_mask:0x3 bank_mask:0xf\n\t"
+      "v_mov_b32_dpp %6, %4 quad_perm:[0,1,2,3] row_mask:0xc bank_mask:0xf\n\t"
+      "v_mov_b32_e32 %3, %2\n\t"
+      "v_mov_b32_e32 %7, %6\n\t"
+      "s_nop 1\n\t"
+      "v_permlane16_swap_b32 %2, %3\n\t"
+      "v_permlane16_swap_b32 %6, %7\n\t"
+      "s_nop 1"
+      : "=&v"(x), "=&v"(y), "=&v"(s0), "=&v"(s1), "=&v"(u), "=&v"(w), "=&v"(t0), "=&v"(t1)
+      : "v"(a), "v"(b));
+  asm("v_max_u32_dpp %0, %3, %6 quad_perm:[0,1,2,3] row_mask:0x1 bank_mask:0xf\n\t"
+      "v_max_u32_dpp %0, %2, %6 quad_perm:[0,1,2,3] row_mask:0x2 bank_mask:0xf\n\t"
+      "v_min_u32_dpp %0, %3, %6 quad_perm:[0,1,2,3] row_mask:0x4 bank_mask:0xf\n\t"
+      "v_min_u32_dpp %0, %2, %6 quad_perm:[0,1,2,3] row_mask:0x8 bank_mask:0xf\n\t"
+      "v_min_u32_dpp %1, %5, %7 quad_perm:[0,1,2,3] row_mask:0x1 bank_mask:0xf\n\t"
+      "v_min_u32_dpp %1, %4, %7 quad_perm:[0,1,2,3] row_mask:0x2 bank_mask:0xf\n\t"
+      "v_max_u32_dpp %1, %5, %7 quad_perm:[0,1,2,3] row_mask:0x4 bank_mask:0xf\n\t"
+      "v_max_u32_dpp %1, %4, %7 quad_perm:[0,1,2,3] row_mask:0x8 bank_mask:0xf"
+      : "=&v"(ra), "=&v"(rb) : "v"(s0), "v"(s1), "v"(t0), "v"(t1), "v"(a), "v"(b));
+  a = ra;
+  b = rb;
+}
+
+template <int J>
+__device__ __forceinline__ void dclean(uint32_t& a, uint32_t& b) {
+  if constexpr (J == 32) d_x32(a, b);
+  if constexpr (J >= 16) d_x16(a, b);
+  if constexpr (J >= 8) d_ror8(a, b);
+  if constexpr (J >= 4) d_x4(a, b);
+  if constexpr (J >= 2) dq_x2(a, b, KEEP_B1);
+  if constexpr (J >= 1) dq_x1(a, b, KEEP_B0);
+}
+
+// a sorted descending and b ascending, in one chain
+__device__ __forceinline__ void sort64_pair(uint32_t& a, uint32_t& b) {
+  dq_x1(a, b, KEEP_B0);
+  dq_x3(a, b, KEEP_B1);
+  dclean<1>(a, b);
+  d_flip8(a, b);
+  dclean<2>(a, b);
+  d_flip16(a, b);
+  dclean<4>(a, b);
+  d_flip32(a, b);
+  dclean<8>(a, b);
+  d_flip64(a, b);
+  dclean<16>(a, b);
+}
+
+}  // namespace flipnet
+
 // Full descending sort of one value per lane (64 values): lane 0 gets the largest.
 template <typename T>
 __device__ __forceinline__ T wave_sort_desc(T v) {
-  return bitonic_levels<64, T>(v);
+  if constexpr (sizeof(T) == 4) return (T)flipnet::sort64<false>((uint32_t)v);
+  else return bitonic_levels<64, T>(v);
 }
 
 // Full ascending sort of one value per lane (every comparator mirrored): lane 0 the smallest.
 template <typename T>
 __device__ __forceinline__ T wave_sort_asc(T v) {
-  return bitonic_levels<64, T, true>(v);
+  if constexpr (sizeof(T) == 4) return (T)flipnet::sort64<true>((uint32_t)v);
+  else return bitonic_levels<64, T, true>(v);
 }
 
 // The descending top 64 of two lists of 64 values, one of each per lane: a sorted descending,
@@ -119,10 +475,16 @@ __device__ __forceinline__ T wave_sort_asc(T v) {
 // both, and the six half-cleaner stages of the last bitonic level sort it.
 template <typename T>
 __device__ __forceinline__ T wave_top64_of_two(T a, T b) {
-  a = wave_sort_desc<T>(a);
-  b = wave_sort_asc<T>(b);
-  const T m = a > b ? a : b;
-  return bitonic_merge_stages<64, 32, T>(m);
+  if constexpr (sizeof(T) == 4) {
+    uint32_t x = (uint32_t)a, y = (uint32_t)b;
+    flipnet::sort64_pair(x, y);
+    return (T)flipnet::clean<32, false>(x > y ? x : y);
+  } else {
+    a = wave_sort_desc<T>(a);
+    b = wave_sort_asc<T>(b);
+    const T m = a > b ? a : b;
+    return bitonic_merge_stages<64, 32, T>(m);
+  }
 }
 
 // Inclusive prefix sum over the 64 lanes in a fixed association: Kogge-Stone inside each

@@ -536,9 +536,29 @@ def test_load_floor_probe_reads_each_waves_share(V):
 
 def test_kernel_attrs_report_every_instantiation_without_spills_in_the_planned_tilings():
     rows = fused_sampling.kernel_attrs()
-    assert len(rows) >= 20
+    # every compiled tiling twice (common, then ",merge"), in the order of the kernel table
+    assert len(rows) % 2 == 0 and len(rows) >= 20
+    half = len(rows) // 2
+    for (n0, c0, t0, *_), (n1, c1, t1, *_) in zip(rows[:half], rows[half:]):
+        assert n1 == n0 + ",merge" and (c0, t0) == (c1, t1)
     for name, chunks, threads, vgprs, scratch, lds, blocks in rows:
-        assert threads in (256, 512, 1024) and vgprs > 0 and lds > 0 and blocks >= 1
+        assert threads in (256, 512, 1024) and 0 < vgprs <= 512 and lds > 0 and blocks >= 1
+        assert name.startswith(f"fsamp_kernel<{threads},{chunks},")
+    # the instantiations the benchmark configurations launch exist and keep every register in
+    # VGPRs (no scratch); C5's tiling holds one 512-thread workgroup per CU
+    by_name = {r[0]: r for r in rows}
+    x = torch.zeros(256, 151936, dtype=torch.bfloat16, device="cuda")
+    for b, v, k in ((1, 151936, 50), (8, 151936, 50), (16, 151936, 256), (16, 151936, 1024),
+                    (256, 151936, 50), (1, 128256, 20), (4, 128256, 50), (16, 128256, 50),
+                    (64, 128256, 50)):
+        pl = fused_sampling.make_plan(x[:b, :v], k)
+        name = f"fsamp_kernel<{pl.threads},{pl.chunks},vec>"
+        if k > 128 and pl.splits > 1:
+            name += ",merge"
+        assert name in by_name, (b, v, k, name)
+        assert by_name[name][4] == 0, f"{name} (B={b}, V={v}, k={k}) spills to scratch"
+    c5 = by_name["fsamp_kernel<512,38,vec>"]
+    assert c5[6] == 1 and c5[3] <= 256
 
 
 def test_wave_primitives_have_the_lane_layouts_the_kernel_assumes():
