@@ -359,7 +359,7 @@ def main() -> int:
 
     import torch
 
-    from llm_sampling_kernel_amd import fused, fused_sampling
+    from llm_sampling_kernel_amd import _lib, fused, fused_sampling
     from llm_sampling_kernel_amd import workloads as W
 
     if not torch.cuda.is_available():
@@ -431,7 +431,18 @@ def main() -> int:
         fused_sampling.probe_load(bufs[i % ROTATE], wave_max)
 
     ms_load = calibrated_ms(load_cold, multiple=ROTATE)["ms"]
-    log(f"C5 floors: one-pass scan {ms_scan * 1e3:.2f}, load only {ms_load * 1e3:.2f} us/call")
+    ti = [0]
+    stream_max = torch.empty(_lib.load().fsamp_probe_stream_words(c5.batch, c5.vocab),
+                             dtype=torch.int32, device="cuda")
+
+    def stream_cold():
+        i = ti[0]
+        ti[0] = i + 1
+        fused_sampling.probe_stream(bufs[i % ROTATE], stream_max)
+
+    ms_stream = calibrated_ms(stream_cold, multiple=ROTATE)["ms"]
+    log(f"C5 floors: one-pass scan {ms_scan * 1e3:.2f}, load only {ms_load * 1e3:.2f}, "
+        f"stream read {ms_stream * 1e3:.2f} us/call")
     B5, V5 = c5.batch, c5.vocab
     gb5 = algo_bytes(B5, V5)
     gbps_cold = gb5 / (ms_cold * 1e-3) / 1e9
@@ -558,6 +569,12 @@ def main() -> int:
                                   "order (512 threads, 38 nontemporal 16-byte loads each, 6 in "
                                   "flight, the slice kept in registers) with only a per-wave "
                                   "maximum after the loads"},
+        "c5_stream_floor": {"us_per_call": round(ms_stream * 1e3, 3),
+                            "gbps": round(gb5 / (ms_stream * 1e-3) / 1e9, 1),
+                            "note": "fsamp_probe_stream: the same batch read once by 4,748 "
+                                    "short workgroups (256 threads x 4 nontemporal 16-byte "
+                                    "loads), no row shape: the read floor of the memory "
+                                    "system"},
         "c5_launches": lc5,
         "configs": others,
         "vocab_parallel": vp,

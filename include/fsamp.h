@@ -292,6 +292,16 @@ int fsamp_probe_scan_rowblock(const void* logits, int dtype, int64_t B, int64_t 
 int fsamp_probe_load(const void* logits, int dtype, int64_t B, int64_t V, uint32_t* wave_max,
                      hipStream_t stream);
 
+/* Pure streaming-read floor of a whole batch (no counterpart in the reference): the contiguous
+ * [B, V] logits read once by short 256-thread workgroups of 4 nontemporal 16-byte loads per
+ * thread (16 KB each, as many as the batch needs), each wave writing the largest order key of
+ * its 4 KB to wave_max (device, fsamp_probe_stream_words(B, V) uint32).  It bounds what any
+ * one-pass kernel can read at, free of a row shape.  Needs a 16-byte-aligned base and
+ * V % 8 == 0 (FSAMP_ERR_VOCAB), and n_words >= fsamp_probe_stream_words (FSAMP_ERR_WORKSPACE). */
+int64_t fsamp_probe_stream_words(int64_t B, int64_t V);
+int fsamp_probe_stream(const void* logits, int dtype, int64_t B, int64_t V, uint32_t* wave_max,
+                       int64_t n_words, hipStream_t stream);
+
 /* One full pass over `splits` workgroups per row, then a per-row merge (two launches);
  * ws needs B*splits*8 bytes.  Replaces probe_scan_split (csrc/probes.cu:108-125). */
 int fsamp_probe_scan_split(const void* logits, int dtype, int64_t B, int64_t V,

@@ -71,6 +71,8 @@ SIGNATURES = {
     "fsamp_probe_scan_rowblock": (_i32, [_vp, _i32, _i64, _i64, _vp, _vp]),
     "fsamp_probe_scan_split": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _sz, _vp]),
     "fsamp_probe_load": (_i32, [_vp, _i32, _i64, _i64, _vp, _vp]),
+    "fsamp_probe_stream_words": (_i64, [_i64, _i64]),
+    "fsamp_probe_stream": (_i32, [_vp, _i32, _i64, _i64, _vp, _i64, _vp]),
     "fsamp_kernel_attrs": (_i32, [ctypes.POINTER(AttrRow), _i32, ctypes.POINTER(_i32)]),
     "fsamp_counter_bytes": (_sz, [_i64]),
     "fsamp_scratch_bytes": (_sz, [_vp, _i64, _i64, _i64, _i64]),

@@ -333,6 +333,22 @@ at::Tensor probe_load(at::Tensor logits, c10::optional<at::Tensor> wave_max) {
   return wm.narrow(0, 0, B * 8).view({B, 8});
 }
 
+at::Tensor probe_stream(at::Tensor logits, c10::optional<at::Tensor> wave_max) {
+  const int dtype = dtype_of(logits);
+  TORCH_CHECK(logits.is_contiguous(), "logits must be a contiguous cuda [B, V] tensor");
+  const int64_t B = logits.size(0), V = logits.size(1);
+  const int64_t n = fsamp_probe_stream_words(B, V);
+  const c10::hip::HIPGuard guard(logits.device().index());
+  at::Tensor wm = wave_max.has_value() ? *wave_max
+                                       : at::empty({n}, logits.options().dtype(at::kInt));
+  TORCH_CHECK(wm.is_cuda() && wm.scalar_type() == at::kInt && wm.is_contiguous(),
+              "wave_max must be a contiguous int32 cuda tensor");
+  check_status(fsamp_probe_stream(logits.data_ptr(), dtype, B, V,
+                                  reinterpret_cast<uint32_t*>(wm.data_ptr()), wm.numel(),
+                                  stream_of(logits)));
+  return wm.narrow(0, 0, n);
+}
+
 // logits_shard: [B, V_shard] with any row stride (a column slice of the whole logits is fine)
 at::Tensor topk_shard(at::Tensor logits_shard, int64_t top_k, int64_t id_offset,
                       int64_t splits_override) {
@@ -424,6 +440,9 @@ PYBIND11_MODULE(_fsamp_torch, m) {
         py::arg("top_k_row") = py::none(), py::arg("top_p_row") = py::none(),
         py::arg("temperature") = py::none(), py::arg("splits_override") = 0,
         py::arg("stages") = false);
+  m.def("probe_stream", &probe_stream,
+        "streaming-read floor of the whole batch: per-wave maximum keys of 4 KB blocks",
+        py::arg("logits"), py::arg("wave_max") = py::none());
   m.def("probe_load", &probe_load, "load-only floor: per-wave maximum keys [B, 8]",
         py::arg("logits"), py::arg("wave_max") = py::none());
   m.def("topk_shard", &topk_shard, "one vocabulary shard: sorted candidate words [B, k]",

@@ -21,7 +21,8 @@ Additions with no counterpart in the reference:
                                     them as open);
   topk_shard / merge_sample         the vocabulary-parallel split of the sampler: per-shard
                                     sorted candidate words, then the merge and draw;
-  probe_load                        the load-only floor of the large-batch launch shape.
+  probe_load                        the load-only floor of the large-batch launch shape;
+  probe_stream                      the streaming-read floor of the whole batch, no row shape.
 """
 
 from __future__ import annotations
@@ -39,6 +40,7 @@ from ._fsamp_torch import (  # noqa: F401
     probe_phase,
     probe_scan_rowblock,
     probe_scan_split,
+    probe_stream,
     sample_fused,
     sample_fused_ex,
     sample_fused_u,

@@ -70,6 +70,19 @@ def test_every_plan_tiles_its_slice_and_fits_the_merge_buffer():
                         assert p.vec == int(ptr % 16 == 0 and V % 8 == 0)
 
 
+def test_stream_probe_sizes_and_refusals_before_any_launch():
+    lib = _lib.load()
+    # 256 x 151936 bf16 = 4,861,952 vectors = 4,748 workgroups of 1,024 vectors, 4 waves each
+    assert lib.fsamp_probe_stream_words(256, 151936) == 4748 * 4
+    assert lib.fsamp_probe_stream_words(3, 1000) == 4          # 375 vectors: one workgroup
+    assert lib.fsamp_probe_stream_words(0, 1000) == 0
+    buf = ctypes.c_void_p(4096)
+    assert lib.fsamp_probe_stream(ctypes.c_void_p(4098), 1, 2, 64, buf, 64, None) == 10  # unaligned
+    assert lib.fsamp_probe_stream(ctypes.c_void_p(4096), 1, 2, 60, buf, 64, None) == 10  # V % 8
+    assert lib.fsamp_probe_stream(ctypes.c_void_p(4096), 1, 2, 64, buf, 3, None) == 6   # too few words
+    assert lib.fsamp_probe_stream(ctypes.c_void_p(4096), 1, 2, 64, None, 64, None) == 7
+
+
 def test_argument_checks_return_the_reference_messages():
     lib = _lib.load()
     assert plan(1, 100, 0)[0] == 3 and b"top_k must be >= 1" == lib.fsamp_error_string(3)
@@ -148,7 +161,8 @@ def test_the_torch_module_is_the_compiled_extension_with_the_reference_surface()
     assert os.path.dirname(os.path.abspath(_fsamp_torch.__file__)) == \
         os.path.dirname(os.path.abspath(_lib.__file__))
     for name in ("sample_fused", "topk_fused", "stages_fused", "probe_phase", "probe_noop",
-                 "probe_scan_rowblock", "probe_scan_split", "kernel_attrs"):
+                 "probe_scan_rowblock", "probe_scan_split", "kernel_attrs", "probe_load",
+                 "probe_stream"):
         assert getattr(fused_sampling, name) is getattr(_fsamp_torch, name)
     x = torch.zeros(2, 64, dtype=torch.bfloat16)  # a CPU tensor: refused before any launch
     with pytest.raises(RuntimeError, match="contiguous cuda"):

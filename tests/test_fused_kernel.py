@@ -534,6 +534,26 @@ def test_load_floor_probe_reads_each_waves_share(V):
     assert np.array_equal(got, want)
 
 
+@pytest.mark.parametrize("B,V", [(5, 151936), (3, 1000), (1, 8)])
+def test_stream_floor_probe_reads_every_block(B, V):
+    # workgroup g reads vectors g*1024 + u*256 + t (u < 4, t < 256), the batch's last vector
+    # standing in past its end; wave w of g holds the lanes t in [64w, 64w + 64)
+    bits = randn_bits((B, V), 95, 3.0, "bfloat16")
+    got = fused_sampling.probe_stream(dev(bits, "bfloat16")).cpu().numpy().view(np.uint32)
+    vmax = O.key16(bits).reshape(-1, 8).max(axis=1)
+    nvec = vmax.size
+    groups = (nvec + 1023) // 1024
+    assert got.size == groups * 4
+    g = np.arange(groups)[:, None, None, None]
+    w = np.arange(4)[None, :, None, None]
+    u = np.arange(4)[None, None, :, None]
+    lane = np.arange(64)[None, None, None, :]
+    idx = np.minimum(g * 1024 + u * 256 + w * 64 + lane, nvec - 1)
+    want = vmax[idx].reshape(groups, 4, -1).max(axis=2).reshape(-1)
+    assert np.array_equal(got, want)
+    assert got.max() == O.key16(bits).max()
+
+
 def test_kernel_attrs_report_every_instantiation_without_spills_in_the_planned_tilings():
     rows = fused_sampling.kernel_attrs()
     # every compiled tiling twice (common, then ",merge"), in the order of the kernel table
