@@ -166,6 +166,7 @@ struct Smem {
   } g;
   uint64_t top[FSAMP_K_MAX];   // gathered candidates, then the sorted top-K of the slice/row
   uint8_t meta[STAGE_SLOTS][NT];  // pair index of each staged pair
+  uint8_t ent[NT / 64][64 * STAGE_SLOTS];  // per wave: its staged (lane << 2 | slot) entries
   union {
     struct {
       uint32_t hist[NSUB * 256];  // radix-fallback histograms (NSUB sub-histograms)
@@ -1516,6 +1517,63 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
     FSAMP_TRACE(12);
   };
 
+  // The streaming path's extraction of the staged pairs, transposed: the wave lists its staged
+  // (lane, slot) entries in LDS, then takes them four at a time, sixteen lanes per entry and one
+  // of the pair's sixteen elements per lane, so that a pass costs the same few instructions
+  // whatever the lanes hold (a lane-per-pair extraction runs its per-element loop for the lane
+  // with the most).  Elements >= L are appended to top[] at slots from one LDS atomic per group
+  // on *cnt.  A lane that staged more pairs than slots sends the wave to extract().
+  auto extract_t = [&](auto c0c, auto c1c, uint32_t L, int nst, int32_t* cnt) {
+    if (__ballot(nst > STAGE_SLOTS) != 0ull) {
+      int unused = 0;
+      extract(c0c, c1c, L, nst, sm.top, FSAMP_K_MAX, cnt, unused);
+      return;
+    }
+    uint8_t* ent = sm.ent[wid];
+    int E = 0;  // wave-uniform
+#pragma unroll
+    for (int s = 0; s < STAGE_SLOTS; ++s) {
+      const uint64_t bs = __ballot(s < nst);
+      if (bs == 0ull) break;
+      if (s < nst) {
+        const int pos = E + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bs >> 32),
+                                                           __builtin_amdgcn_mbcnt_lo((uint32_t)bs, 0u));
+        ent[pos] = (uint8_t)((lane << 2) | s);
+      }
+      E += (int)__popcll(bs);
+    }
+    if (E == 0) return;
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    const int j = lane & 15;   // element of the pair: chunk j >> 3, position j & 7
+    const int eo = lane >> 4;  // entry within a group of four
+    for (int e0 = 0; e0 < E; e0 += 4) {
+      const int e = e0 + eo;
+      bool ok = false;
+      uint64_t word = 0ull;
+      if (e < E) {
+        const uint32_t en = ent[e];
+        const int ts = wid * 64 + (int)(en >> 2);  // the thread that staged the pair
+        const int sl = (int)(en & 3u);
+        const uint16_t* src = j < 8 ? reinterpret_cast<const uint16_t*>(&sm.g.st.a[sl][ts])
+                                    : reinterpret_cast<const uint16_t*>(&sm.g.st.b[sl][ts]);
+        const uint32_t key = src[j & 7];
+        const int c = 2 * (int)sm.meta[sl][ts] + (j >> 3);
+        ok = key >= L;
+        word = pack(key, (uint32_t)(lo + (c * NT + ts) * 8 + (j & 7)));
+      }
+      const uint64_t b = __ballot(ok);
+      if (b == 0ull) continue;
+      int base = 0;
+      if (lane == 0) base = atomicAdd(cnt, (int)__popcll(b));
+      base = __builtin_amdgcn_readlane(base, 0);
+      if (ok) {
+        const int slot = base + (int)__builtin_amdgcn_mbcnt_hi(
+                                    (uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+        if (slot < FSAMP_K_MAX) sm.top[slot] = word;
+      }
+    }
+  };
+
   // candidates >= L of chunk pair i appended to top[] (capacity FSAMP_K_MAX; more are counted,
   // not written) at slots from one LDS atomic per wave on *cnt; used for the last pair of the
   // streaming path, whose data lands last (one compare and one scalar branch when the wave has
@@ -1621,10 +1679,9 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
       // from registers, the only gather after the last byte.  After the barrier the candidates
       // are top[0, total): wave 0 reads them without compacting per-wave lists.
       int32_t* cnt = &sm.misc[M_CNT];
-      int unused = 0;
       int nst = 0;
       stage(IC<0>{}, IC<PB / 2>{}, L, nst);
-      extract(IC<0>{}, IC<PB>{}, L, nst, sm.top, FSAMP_K_MAX, cnt, unused);
+      extract_t(IC<0>{}, IC<PB>{}, L, nst, cnt);
       constexpr int LASTP = NP - 1;  // the last pair (chunk 2*LASTP, and 2*LASTP + 1 if < CH)
       int nst2 = 0;
       static_for<PB, CH>([&](auto cc) {
@@ -1637,7 +1694,7 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
         if constexpr (((c & 1) == 1 || c == CH - 1) && c / 2 < LASTP)
           stage(IC<c / 2>{}, IC<c / 2 + 1>{}, L, nst2);
         if constexpr (c == 2 * LASTP - 1)  // every middle pair staged: gather them
-          extract(IC<PB>{}, IC<2 * LASTP>{}, L, nst2, sm.top, FSAMP_K_MAX, cnt, unused);
+          extract_t(IC<PB>{}, IC<2 * LASTP>{}, L, nst2, cnt);
       });
       FSAMP_WTRACE(pm[NP - 1]);
       gather_pair(IC<LASTP>{}, L, cnt);
