@@ -24,26 +24,36 @@ size_t round_up(size_t a, size_t b) { return (a + b - 1) / b * b; }
 size_t counter_bytes(int64_t B) { return round_up((size_t)B * TICKET_STRIDE * 4u, 256); }
 constexpr size_t kGridCounterBytes = 256;  // the grid counter of the in-kernel offset advance
 
-// Split count when the caller does not force one: one workgroup per row once the batch alone
-// fills half the CUs; below that, splits shorten each workgroup's selection chain (the
-// slice's candidates, gather and sort shrink with it) at the price of one more list in the
-// row merge.  Measured on MI355X (per call, k=50): V=151936 bf16 at B=1 10.35 / 10.38 /
-// 9.97 / 10.45 us for S=4/5/6/7, and with 64-value ties at B=8 16.2 / 13.4 / 12.6 us for
-// S=4/5/6; V=128256 fp16 at B=1 9.2 / 9.8 / 9.6 us for S=4/5/6 and at B=64 11.3 / 10.5 us
-// for S=2/4.
-int auto_splits(int64_t B, int64_t V) {
-  if (B >= 128) return 1;
-  if (B >= 64) return 4;
-  return V > 131072 ? 6 : 4;
+// Split count when the caller does not force one.  Splits shorten each workgroup's selection
+// chain (the slice's candidates, gather and sort shrink with it) at the price of one more list
+// in the row merge, but a grid of more workgroups than MI355X's 256 CUs runs in two waves (the
+// large tilings hold one workgroup per CU), which costs far more than any split saves.  So the
+// splits of a batch add up to at most 128 workgroups for k <= 128 (256 for wider k, whose
+// selection is longer), and at most 6 (V > 131072) or 4 per row.  Measured on MI355X (per call,
+// graph replay, from the (threads, splits) sweep): V=151936 bf16 k=50 at B=48 12.2 / 12.0 /
+// 18.4 us for S=2/3/6 and at B=96 14.4 / 13.7 / 20.2 us for S=1/2/4; V=128256 fp16 k=50 at
+// B=64 12.9 / 11.9 / 12.3 us for S=1/2/4 and at B=96 12.8 / 19.2 us for S=1/4; B=1 k=50 at
+// V=151936 10.35 / 9.97 / 10.45 us for S=4/6/7; with 64-value ties at B=8 16.2 / 12.6 us for
+// S=4/6; k=256 at B=1..64 with 1024 threads 15.7-16.4 us for S=4, against 16.4-17.1 us for the
+// 512-thread plans.
+int auto_splits(int64_t B, int64_t V, int K) {
+  const int64_t grid = K > 128 ? 256 : 128;
+  const int64_t most = K > 128 ? 4 : (V > 131072 ? 6 : 4);
+  return (int)std::max<int64_t>(1, std::min<int64_t>(most, grid / B));
 }
 
 // Workgroup size for a slice: 256 threads while 8 chunks per thread hold it, then 512 (up to
-// 38 chunks, 8 waves with room for the slice in VGPRs), then 1024; `force` (a tuning override)
-// replaces the choice; never fewer threads than k (the slice's lower bound ranks one maximum
-// per thread and the candidate sort one candidate per thread).
+// 38 chunks, 8 waves with room for the slice in VGPRs), then 1024; for k > 128, 1024 while 8
+// chunks per thread hold the slice (the wide selection's histograms, ranking and merge run over
+// the whole workgroup); `force` (a tuning override) replaces the choice; never fewer threads
+// than k (the slice's lower bound ranks one maximum per thread and the candidate sort one
+// candidate per thread).
 int preferred_threads(int slice, int K, int force) {
-  int want = force > 0 ? force
-             : (slice <= 256 * 8 * 8 ? 256 : (slice <= 512 * 8 * 38 ? 512 : 1024));
+  int want = force > 0                              ? force
+             : K > 128 && slice <= 1024 * 8 * 8     ? 1024
+             : slice <= 256 * 8 * 8                 ? 256
+             : slice <= 512 * 8 * 38                ? 512
+                                                    : 1024;
   while (want < K) want *= 2;
   return want;
 }
@@ -82,7 +92,7 @@ int make_plan_impl(const void* logits, int64_t B, int64_t V, int64_t ld, int64_t
   const int K = (int)pl->k;
   const bool vec = ((uintptr_t)logits % 16 == 0) && (V % 8 == 0) && (ld % 8 == 0);
   const int units = (int)((V + 7) / 8);
-  int S = splits_override > 0 ? (int)std::min<int64_t>(splits_override, 1 << 20) : auto_splits(B, V);
+  int S = splits_override > 0 ? (int)std::min<int64_t>(splits_override, 1 << 20) : auto_splits(B, V, K);
   // the row's last workgroup merges S*K words in LDS, ranking across at most MAX_SPLITS lists
   S = std::max(1, std::min({S, CAND_CAP / K, MAX_SPLITS, units}));
   const KernelEntry* e = nullptr;

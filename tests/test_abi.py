@@ -42,9 +42,15 @@ def plan(B, V, k, splits=0, ptr=4096):
 
 @pytest.mark.parametrize("B,V,k,S,threads", [
     (1, 151936, 50, 6, 512),      # C1: 6 splits of 25328 elements
-    (64, 128256, 50, 4, 512),     # C2, B=64: 4 splits of 32064
+    (16, 128256, 50, 4, 512),     # C2, B=16: 4 splits of 32064
+    (64, 128256, 50, 2, 512),     # C2, B=64: 2 splits (128 workgroups)
+    (48, 151936, 50, 2, 512),     # B * S stays within 128 workgroups for k <= 128
+    (96, 151936, 50, 1, 512),     #   (so that the grid runs in one wave of the 256 CUs)
+    (8, 151936, 50, 6, 512),      # C3
+    (16, 151936, 256, 4, 1024),   # C4 k=256: wide k takes 1024 threads, 4 splits
     (16, 151936, 1024, 4, 1024),  # C4 k=1024: 4 splits, 4096 merged words
     (256, 151936, 50, 1, 512),    # C5: one workgroup per row, slice in VGPRs
+    (256, 151936, 256, 1, 512),   # wide k over a whole row: the 512-thread register tiling
 ])
 def test_plans_for_the_benchmark_shapes(B, V, k, S, threads):
     rc, p = plan(B, V, k)
