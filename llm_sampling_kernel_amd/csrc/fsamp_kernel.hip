@@ -1663,7 +1663,7 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
     //   L = the lower bound from the maxima of chunks 0..PB-1 (valid for the whole slice: the
     //   prefix alone holds keff distinct elements >= L); the prefix's candidates are staged and
     //   gathered while the last loads are in flight, the rest once it has landed; wave 0 then
-    //   takes the top 64 of the (on C5, 70 to 124) candidates in registers.  More than 128
+    //   takes the top 64 of the (on C5, 70 to 124) candidates in registers.  More than 256
     //   falls back to the general selection below with the bound of the whole slice.
     if (count > 0 && keff <= 64 && p.stop >= 2) {
       const uint32_t L = lower_bound(tmax_of(IC<0>{}, IC<PB / 2>{}));
@@ -1705,19 +1705,28 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
         if (t == 0 && split == 0) p.out[row] = total;
         return;
       }
-      if (total <= 128) {
+      if (total <= 256) {
         if (wid != 0) return;
         FSAMP_TRACE(14);
         auto cand = [&](int e) -> uint64_t { return e < total ? sm.top[e] : 0ull; };
         uint64_t v[1];
-        if (total <= 64) v[0] = wave_sort64_words(cand(lane), L, p.V);
-        else v[0] = wave_top64_of128(cand(lane), cand(64 + lane), L, p.V);
+        if (total <= 64) {
+          v[0] = wave_sort64_words(cand(lane), L, p.V);
+        } else if (total <= 128) {
+          v[0] = wave_top64_of128(cand(lane), cand(64 + lane), L, p.V);
+        } else {
+          // 129 to 256 (a tail of noisy rows, or ties at the bound): the top 64 of each half,
+          // then of the two
+          const uint64_t lo = wave_top64_of128(cand(lane), cand(64 + lane), L, p.V);
+          const uint64_t hi = wave_top64_of128(cand(128 + lane), cand(192 + lane), L, p.V);
+          v[0] = wave_top64_of128(lo, hi, L, p.V);
+        }
         if (lane >= keff) v[0] = 0ull;
         const RowCtl rc = row_ctl();
         wave_tail_regs<1, NT>(p, sm, v, keff, row, split, rc, p.S);
         return;
       }
-      // Too many candidates for the register sort (heavy ties near the bound): the general
+      // Too many candidates for the register sorts (heavy ties near the bound): the general
       // selection with the bound of the whole slice, on the slice read again from memory.  The
       // reload keeps the streamed chunks dead once gathered, so the registers they held are
       // free for the sort and the tail of the common case.  Every wave has read the total

@@ -897,6 +897,39 @@ def test_large_batch_rows_through_the_streaming_selection(V, k):
     assert np.array_equal(ren.view(np.uint32), want.renormed.view(np.uint32))
 
 
+def _tied_top_rows(V, seed):
+    """128 rows of N(0, 1) noise with T equal top values (+20) spread over each row, T from 100
+    to 320: the streaming selection's bound lands on the tied value, so a row has about T
+    candidates (more where few of the ties fall in the prefix), across the register sorts'
+    limits of 128 and 256 candidates."""
+    g = np.random.Generator(np.random.PCG64(seed))
+    x = g.standard_normal((128, V)).astype(np.float32)
+    for r in range(128):
+        t = 100 + (r * 220) // 127
+        pos = np.linspace(0, V - 1, t).astype(np.int64) + g.integers(0, V // t, t) // 2
+        x[r, np.minimum(pos, V - 1)] = 20.0
+    return x
+
+
+@pytest.mark.parametrize("V", [151936, 128256])
+@pytest.mark.parametrize("k", [20, 50, 64])
+def test_streaming_rows_with_129_to_256_candidates_sort_in_registers(V, k):
+    bits = W.to_bits(_tied_top_rows(V, 8400 + k), "bfloat16")
+    x = dev(bits, "bfloat16")
+    assert fused_sampling.make_plan(x, k).splits == 1
+    counts = fused_sampling.probe_phase(x, k, 0.9, 3, 0).cpu().numpy()
+    # the rows span all three cases: the 128-candidate sort, the 256-candidate one, the re-read
+    hist = ((counts <= 128).sum(), ((counts > 128) & (counts <= 256)).sum(), (counts > 256).sum())
+    assert hist[0] >= 1 and hist[1] >= 40 and hist[2] >= 8, hist
+    un = ustream(128, 8500 + k)
+    want = oracle(bits, "bfloat16", k, 0.9, un)
+    assert np.array_equal(fused.topk_fused(x, k).cpu().numpy(), want.topk_ids)
+    tok, ids, keep, ren = run_u(x, k, 0.9, un)
+    assert np.array_equal(tok, want.token_ids)
+    assert np.array_equal(keep, want.keep)
+    assert np.array_equal(ren.view(np.uint32), want.renormed.view(np.uint32))
+
+
 def test_sixteen_split_hand_off_at_b256():
     # the most workgroups per row (16) on the largest batch: 4096 workgroups whose row
     # tickets and candidate lists must hand over exactly once per row
