@@ -1383,13 +1383,19 @@ __global__ __launch_bounds__(NT) void fsamp_kernel(Params p) {
 
   // 2. lower bound L of the keff-th largest key among the given thread maxima (keff <= NT by
   //    plan): the keff-th largest of the union of every wave's top-m thread maxima,
-  //    m = max(ceil(keff/W), 64/W).  Maxima are made unique by the thread index in the low
-  //    bits.  Each wave sorts its 64 maxima with the DPP network and publishes the top m;
+  //    m = max(ceil(keff/W), 64/W), doubled for keff <= 64 when that leaves fewer than 8
+  //    published words beyond the keff-th: with no slack the bound is the smallest published
+  //    maximum, which one wave holding fewer than its share of the top maxima pulls far down,
+  //    and the streaming selection's rows then pass its 256-candidate sort (k=64 at B=256: 32.5
+  //    against 19.9 us; for k > 64 the larger kth sort costs more than the tighter bound saves,
+  //    k=65 at B=256: 21.5 against 20.2 us).  Maxima are made unique by the thread index in the
+  //    low bits.  Each wave sorts its 64 maxima with the DPP network and publishes the top m;
   //    after one barrier every wave sorts the W*m published words itself (no second barrier).
   //    Past 256 published words (keff > 256) the group bound above is used instead, which
   //    keeps the register sort of more than 256 words out of the phase that holds the slice.
   auto lower_bound = [&](uint32_t tm) -> uint32_t {
-    const int m = min(64, max((keff + W - 1) / W, 64 / W));
+    int m = min(64, max((keff + W - 1) / W, 64 / W));
+    if (keff <= 64 && W * m - keff < 8 && 2 * W * m <= WSORT_MAX) m *= 2;
     const int n = W * m;
     if (n > WSORT_MAX) return group_bound();
     const uint32_t srt = wave_sort_desc<uint32_t>((tm << 10) | (uint32_t)t);

@@ -930,6 +930,21 @@ def test_streaming_rows_with_129_to_256_candidates_sort_in_registers(V, k):
     assert np.array_equal(ren.view(np.uint32), want.renormed.view(np.uint32))
 
 
+@pytest.mark.parametrize("k", [57, 64])
+def test_the_prefix_bound_keeps_noise_rows_within_the_register_sorts_up_to_k64(k):
+    # with as many published thread maxima as k the bound would be the smallest of them and
+    # noise rows would pass 256 candidates (the slice re-read); with the slack kept, none do
+    bits = randn_bits((128, 151936), 8600 + k, 3.0, "bfloat16")
+    x = dev(bits, "bfloat16")
+    assert fused_sampling.make_plan(x, k).splits == 1
+    counts = fused_sampling.probe_phase(x, k, 0.9, 3, 0).cpu().numpy()
+    assert counts.min() >= k and counts.max() <= 256, (counts.min(), counts.max())
+    un = ustream(128, 8700 + k)
+    want = oracle(bits, "bfloat16", k, 0.9, un)
+    tok, ids, keep, ren = run_u(x, k, 0.9, un)
+    assert np.array_equal(tok, want.token_ids)
+
+
 def test_sixteen_split_hand_off_at_b256():
     # the most workgroups per row (16) on the largest batch: 4096 workgroups whose row
     # tickets and candidate lists must hand over exactly once per row
