@@ -47,11 +47,17 @@ int auto_splits(int64_t B, int64_t V, int K) {
 // chunks per thread hold the slice (the wide selection's histograms, ranking and merge run over
 // the whole workgroup); `force` (a tuning override) replaces the choice; never fewer threads
 // than k (the slice's lower bound ranks one maximum per thread and the candidate sort one
-// candidate per thread).
-int preferred_threads(int slice, int K, int force) {
+// candidate per thread).  A slice that 512 threads would hold in 32 chunks (V = 128256 or
+// 131072 in one slice) takes 1024 threads x 16 chunks while the grid has at most 192
+// workgroups: measured per call (graph replay) at V=128256 k=50 bf16, 11.6 / 11.9 / 12.7 us
+// against 12.8 / 12.6 / 14.4 us at B = 96 / 128 / 192 (sixteen waves per CU keep more loads in
+// flight); from B = 224 on the two measure alike at V=128256, and at V=131072 the 512-thread
+// tiling is 1-2 us faster.
+int preferred_threads(int slice, int K, int force, int64_t grid) {
   int want = force > 0                              ? force
              : K > 128 && slice <= 1024 * 8 * 8     ? 1024
              : slice <= 256 * 8 * 8                 ? 256
+             : slice > 512 * 8 * 24 && slice <= 1024 * 8 * 16 && grid <= 192 ? 1024
              : slice <= 512 * 8 * 38                ? 512
                                                     : 1024;
   while (want < K) want *= 2;
@@ -60,8 +66,8 @@ int preferred_threads(int slice, int K, int force) {
 
 // Smallest compiled tiling of the preferred workgroup size that holds `slice` elements; when
 // that size has none large enough, the smallest-capacity tiling of any size (unless forced).
-const KernelEntry* pick_tiling(int slice, int vec, int K, int force) {
-  const int want = preferred_threads(slice, K, force);
+const KernelEntry* pick_tiling(int slice, int vec, int K, int force, int64_t grid) {
+  const int want = preferred_threads(slice, K, force, grid);
   const KernelEntry* best = nullptr;
   const KernelEntry* any = nullptr;
   for (int i = 0; i < kNumKernels; ++i) {
@@ -99,7 +105,7 @@ int make_plan_impl(const void* logits, int64_t B, int64_t V, int64_t ld, int64_t
   int slice = 0;
   for (;;) {
     slice = ((units + S - 1) / S) * 8;
-    e = pick_tiling(slice, vec ? 1 : 0, K, force_threads);
+    e = pick_tiling(slice, vec ? 1 : 0, K, force_threads, B * (int64_t)S);
     if (e != nullptr) break;
     if (S >= CAND_CAP / K || S >= MAX_SPLITS || S >= units) return FSAMP_ERR_VOCAB;
     ++S;

@@ -44,6 +44,8 @@ def plan(B, V, k, splits=0, ptr=4096):
     (1, 151936, 50, 6, 512),      # C1: 6 splits of 25328 elements
     (16, 128256, 50, 4, 512),     # C2, B=16: 4 splits of 32064
     (64, 128256, 50, 2, 512),     # C2, B=64: 2 splits (128 workgroups)
+    (128, 128256, 50, 1, 1024),   # a 32-chunk slice on a grid of <= 192 takes 1024 x 16
+    (256, 128256, 50, 1, 512),    #   and beyond that the 512-thread streaming tiling
     (48, 151936, 50, 2, 512),     # B * S stays within 128 workgroups for k <= 128
     (96, 151936, 50, 1, 512),     #   (so that the grid runs in one wave of the 256 CUs)
     (8, 151936, 50, 6, 512),      # C3

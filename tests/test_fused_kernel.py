@@ -885,10 +885,14 @@ def _streaming_rows(V, seed):
 @pytest.mark.parametrize("V", [151936, 128256])
 @pytest.mark.parametrize("k", [1, 20, 50, 64, 65])
 def test_large_batch_rows_through_the_streaming_selection(V, k):
-    bits = W.to_bits(_streaming_rows(V, 8100 + k), "bfloat16")
+    rows = _streaming_rows(V, 8100 + k)
+    if V == 128256:  # 256 rows: the streaming tiling (a grid of <= 192 takes 1024 x 16)
+        rows = np.concatenate([rows, _streaming_rows(V, 9100 + k)])
+    bits = W.to_bits(rows, "bfloat16")
     x = dev(bits, "bfloat16")
-    assert fused_sampling.make_plan(x, k).splits == 1
-    un = ustream(128, 8200 + k)
+    pl = fused_sampling.make_plan(x, k)
+    assert pl.splits == 1 and pl.threads == 512
+    un = ustream(bits.shape[0], 8200 + k)
     want = oracle(bits, "bfloat16", k, 0.9, un)
     assert np.array_equal(fused.topk_fused(x, k).cpu().numpy(), want.topk_ids)
     tok, ids, keep, ren = run_u(x, k, 0.9, un)
@@ -914,14 +918,18 @@ def _tied_top_rows(V, seed):
 @pytest.mark.parametrize("V", [151936, 128256])
 @pytest.mark.parametrize("k", [20, 50, 64])
 def test_streaming_rows_with_129_to_256_candidates_sort_in_registers(V, k):
-    bits = W.to_bits(_tied_top_rows(V, 8400 + k), "bfloat16")
+    rows = _tied_top_rows(V, 8400 + k)
+    if V == 128256:  # 256 rows: the streaming tiling (a grid of <= 192 takes 1024 x 16)
+        rows = np.concatenate([rows, _tied_top_rows(V, 9400 + k)])
+    bits = W.to_bits(rows, "bfloat16")
     x = dev(bits, "bfloat16")
-    assert fused_sampling.make_plan(x, k).splits == 1
+    pl = fused_sampling.make_plan(x, k)
+    assert pl.splits == 1 and pl.threads == 512
     counts = fused_sampling.probe_phase(x, k, 0.9, 3, 0).cpu().numpy()
     # the rows span all three cases: the 128-candidate sort, the 256-candidate one, the re-read
     hist = ((counts <= 128).sum(), ((counts > 128) & (counts <= 256)).sum(), (counts > 256).sum())
     assert hist[0] >= 1 and hist[1] >= 40 and hist[2] >= 8, hist
-    un = ustream(128, 8500 + k)
+    un = ustream(bits.shape[0], 8500 + k)
     want = oracle(bits, "bfloat16", k, 0.9, un)
     assert np.array_equal(fused.topk_fused(x, k).cpu().numpy(), want.topk_ids)
     tok, ids, keep, ren = run_u(x, k, 0.9, un)
