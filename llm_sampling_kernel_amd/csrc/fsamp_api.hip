@@ -33,7 +33,9 @@ constexpr size_t kGridCounterBytes = 256;  // the grid counter of the in-kernel 
 // 1: short rows gain less from a shorter chain than the hand-off and merge cost (V=32000 k=50 at
 // B=1 / 16 / 64: 6.2 / 6.7 / 7.8 us unsplit against 8.4 / 8.5 / 9.2 us with 4 splits; V=50304
 // at B=1 7.6 against 9.1 us), long ones more (V=256000 at B=1: 9.9 us with 8 splits, 10.3 with
-// 6; V=202048: 9.9 against 10.7 us).  Measured on MI355X (per call,
+// 6; V=202048: 9.9 against 10.7 us).  For 64 < k <= 128 (two ranks per lane in the merge) at
+// most 4: V=151936 k=128 at B=1 / 16, 15.3 / 15.4 us against 15.7 / 16.0 us with 6 splits.
+// Measured on MI355X (per call,
 // graph replay, from the (threads, splits) sweep): V=151936 bf16 k=50 at B=48 12.2 / 12.0 /
 // 18.4 us for S=2/3/6 and at B=96 14.4 / 13.7 / 20.2 us for S=1/2/4; V=128256 fp16 k=50 at
 // B=64 12.9 / 11.9 / 12.3 us for S=1/2/4 and at B=96 12.8 / 19.2 us for S=1/4; B=1 k=50 at
@@ -42,7 +44,9 @@ constexpr size_t kGridCounterBytes = 256;  // the grid counter of the in-kernel 
 // 512-thread plans.
 int auto_splits(int64_t B, int64_t V, int K) {
   const int64_t grid = K > 128 ? 256 : 128;
-  const int64_t most = K > 128 ? 4 : V > 196608 ? 8 : V > 131072 ? 6 : V > 65536 ? 4 : 1;
+  const int64_t most = K > 128  ? 4
+                       : K > 64  ? (V > 65536 ? 4 : 1)
+                       : V > 196608 ? 8 : V > 131072 ? 6 : V > 65536 ? 4 : 1;
   return (int)std::max<int64_t>(1, std::min<int64_t>(most, grid / B));
 }
 
