@@ -42,9 +42,14 @@ constexpr size_t kGridCounterBytes = 256;  // the grid counter of the in-kernel 
 // V=151936 10.35 / 9.97 / 10.45 us for S=4/6/7; with 64-value ties at B=8 16.2 / 12.6 us for
 // S=4/6; k=256 at B=1..64 with 1024 threads 15.7-16.4 us for S=4, against 16.4-17.1 us for the
 // 512-thread plans.
-int auto_splits(int64_t B, int64_t V, int K) {
-  const int64_t grid = K > 128 ? 256 : 128;
+// Rows read element by element (not 16-byte aligned, V % 8 != 0) take the small element
+// tilings, which gain from more splits at every row length: up to 8, within 256 workgroups
+// (V=50257 k=50 at B = 1 / 16 / 64 / 128: 11.4 / 12.2 / 15.4 / 17.7 us with 8 / 8 / 4 / 2
+// splits, against 19.4 / 20.6 / 20.7 / 20.8 us unsplit).
+int auto_splits(int64_t B, int64_t V, int K, bool vec) {
+  const int64_t grid = K > 128 || !vec ? 256 : 128;
   const int64_t most = K > 128  ? 4
+                       : !vec   ? 8
                        : K > 64  ? (V > 65536 ? 4 : 1)
                        : V > 196608 ? 8 : V > 131072 ? 6 : V > 65536 ? 4 : 1;
   return (int)std::max<int64_t>(1, std::min<int64_t>(most, grid / B));
@@ -106,7 +111,7 @@ int make_plan_impl(const void* logits, int64_t B, int64_t V, int64_t ld, int64_t
   const int K = (int)pl->k;
   const bool vec = ((uintptr_t)logits % 16 == 0) && (V % 8 == 0) && (ld % 8 == 0);
   const int units = (int)((V + 7) / 8);
-  int S = splits_override > 0 ? (int)std::min<int64_t>(splits_override, 1 << 20) : auto_splits(B, V, K);
+  int S = splits_override > 0 ? (int)std::min<int64_t>(splits_override, 1 << 20) : auto_splits(B, V, K, vec);
   // the row's last workgroup merges S*K words in LDS, ranking across at most MAX_SPLITS lists
   S = std::max(1, std::min({S, CAND_CAP / K, MAX_SPLITS, units}));
   const KernelEntry* e = nullptr;
