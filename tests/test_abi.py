@@ -53,6 +53,9 @@ def plan(B, V, k, splits=0, ptr=4096):
     (16, 151936, 1024, 4, 1024),  # C4 k=1024: 4 splits, 4096 merged words
     (256, 151936, 50, 1, 512),    # C5: one workgroup per row, slice in VGPRs
     (256, 151936, 256, 1, 512),   # wide k over a whole row: the 512-thread register tiling
+    (1, 32000, 50, 1, 512),       # short rows are not split (V <= 65536)
+    (1, 256000, 50, 8, 512),      # long rows take up to 8 splits (V > 196608)
+    (16, 151936, 128, 4, 512),    # 64 < k <= 128: at most 4 splits
 ])
 def test_plans_for_the_benchmark_shapes(B, V, k, S, threads):
     rc, p = plan(B, V, k)
@@ -60,6 +63,13 @@ def test_plans_for_the_benchmark_shapes(B, V, k, S, threads):
     assert p.threads * p.chunks * 8 >= p.slice and p.slice * p.splits >= V
     assert p.slice % 8 == 0 and p.vec == 1
     assert p.workspace_bytes == ((128 * B + 255) // 256) * 256 + 256 + (0 if S == 1 else B * S * k * 8)
+
+
+@pytest.mark.parametrize("B,S", [(1, 8), (16, 8), (64, 4), (128, 2), (256, 1)])
+def test_rows_read_by_element_split_up_to_eight_ways_within_256_workgroups(B, S):
+    rc, p = plan(B, 50257, 50)
+    assert rc == 0 and p.vec == 0 and p.splits == S
+    assert p.threads * p.chunks * 8 >= p.slice and (S - 1) * p.slice < 50257 <= S * p.slice
 
 
 def test_every_plan_tiles_its_slice_and_fits_the_merge_buffer():
