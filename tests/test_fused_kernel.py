@@ -953,6 +953,23 @@ def test_the_prefix_bound_keeps_noise_rows_within_the_register_sorts_up_to_k64(k
     assert np.array_equal(tok, want.token_ids)
 
 
+@pytest.mark.parametrize("k", [1, 50, 64, 100])
+def test_32_chunk_rows_on_small_grids_take_1024_thread_workgroups(k):
+    # V = 128256 in one slice at B <= 192: the planner's 1024 x 16 tiling (non-streaming)
+    rows = _streaming_rows(128256, 8800 + k)
+    bits = W.to_bits(rows, "bfloat16")
+    x = dev(bits, "bfloat16")
+    pl = fused_sampling.make_plan(x, k)
+    assert pl.splits == 1 and pl.threads == 1024 and pl.chunks == 16
+    un = ustream(128, 8900 + k)
+    want = oracle(bits, "bfloat16", k, 0.9, un)
+    assert np.array_equal(fused.topk_fused(x, k).cpu().numpy(), want.topk_ids)
+    tok, ids, keep, ren = run_u(x, k, 0.9, un)
+    assert np.array_equal(tok, want.token_ids)
+    assert np.array_equal(keep, want.keep)
+    assert np.array_equal(ren.view(np.uint32), want.renormed.view(np.uint32))
+
+
 def test_sixteen_split_hand_off_at_b256():
     # the most workgroups per row (16) on the largest batch: 4096 workgroups whose row
     # tickets and candidate lists must hand over exactly once per row
