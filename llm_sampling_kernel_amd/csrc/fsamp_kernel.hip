@@ -167,6 +167,7 @@ struct Smem {
   uint64_t top[FSAMP_K_MAX];   // gathered candidates, then the sorted top-K of the slice/row
   uint8_t meta[STAGE_SLOTS][NT];  // pair index of each staged pair
   uint8_t ent[NT / 64][64 * STAGE_SLOTS];  // per wave: its staged (lane << 2 | slot) entries
+  static_assert(STAGE_SLOTS <= 4, "an entry keeps its slot in two bits");
   union {
     struct {
       uint32_t hist[NSUB * 256];  // radix-fallback histograms (NSUB sub-histograms)
